@@ -1,0 +1,182 @@
+/*
+ * kvdec.h -- C ABI of the MI355X (gfx950) decode-attention library
+ * (libkvdec.so).
+ *
+ * One entry point per operator of the reference's decode-attention path.  The
+ * reference is Python + Triton, so its "interface" is the Python function each
+ * entry point replaces; the citation next to each declaration names it
+ * (paths relative to the reference repository root).
+ *
+ * Conventions (all entry points):
+ *   - every data pointer is a device pointer; tensors are dense row-major
+ *     (contiguous) in the shapes stated below;
+ *   - `stream` is a hipStream_t (NULL = the null stream); work is enqueued
+ *     asynchronously and nothing synchronises;
+ *   - the library never allocates device memory: split-K partials live in a
+ *     caller-supplied workspace of kvdec_workspace_bytes() bytes;
+ *   - return 0 on success, a negative KVDEC_E* code when host-side argument
+ *     validation fails (nothing is launched, no HIP call is made), or a
+ *     positive hipError_t value when a launch fails;
+ *   - stateless and reentrant: no global state besides what the HIP runtime
+ *     keeps.
+ */
+#ifndef KVDEC_H_
+#define KVDEC_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes (negative: rejected before launch) -------------------- */
+#define KVDEC_OK 0
+#define KVDEC_E_NULL (-1)        /* a required pointer is NULL                 */
+#define KVDEC_E_SHAPE (-2)       /* a dimension is out of range / inconsistent */
+#define KVDEC_E_DTYPE (-3)       /* unsupported element type                   */
+#define KVDEC_E_GROUP (-4)       /* token count not a multiple of the group    */
+#define KVDEC_E_DGROUP (-5)      /* head dim not a multiple of the group       */
+#define KVDEC_E_WORKSPACE (-6)   /* workspace missing or too small             */
+#define KVDEC_E_WINDOW (-7)      /* window / sink / residual combination       */
+#define KVDEC_E_SEQLEN (-8)      /* seq_len < 1                                */
+#define KVDEC_E_BITS (-9)        /* only 2-bit codes are implemented           */
+#define KVDEC_E_UNSUPPORTED (-10)/* valid but not implemented (group != 32 ...) */
+
+/* ---- element types --------------------------------------------------- */
+#define KVDEC_F16 0
+#define KVDEC_F32 1
+#define KVDEC_BF16 2
+
+/* ---- sparse cache layouts -------------------------------------------- */
+#define KVDEC_LAYOUT_LINEAR 0    /* reference: slot s >= sink holds position
+                                    (seq_len - window) + (s - sink)          */
+#define KVDEC_LAYOUT_RING 1      /* position p >= sink in slot
+                                    sink + (p - sink) mod window              */
+
+/* ---- workspace kinds ------------------------------------------------- */
+#define KVDEC_KIND_DENSE 0       /* n_slots = seq_len                          */
+#define KVDEC_KIND_SPARSE 1      /* n_slots = sink + window                    */
+#define KVDEC_KIND_KIVI 2        /* n_slots = window                           */
+
+/* Human-readable text for any return code (never NULL). */
+const char* kvdec_strerror(int code);
+
+/* Library version string, e.g. "kvdec 0.1 gfx950". */
+const char* kvdec_version(void);
+
+/* Number of split-K partitions the attention entry points use for this
+ * problem (1 = single pass, no workspace).  Pure arithmetic, no HIP call. */
+int kvdec_num_splits(int kind, int64_t B, int32_t KVH, int64_t n_slots);
+
+/* Workspace bytes the attention entry point of `kind` needs (0 when a
+ * single pass suffices).  Pure arithmetic, no HIP call. */
+size_t kvdec_workspace_bytes(int kind, int64_t B, int32_t H, int32_t KVH,
+                             int64_t n_slots, int32_t D);
+
+/*
+ * Dense causal GQA decode: one query token per (batch, head) against the
+ * whole context.  Replaces dense_kernel.py:70-82 (dense_decode_attention)
+ * and its kernel dense_kernel.py:21-67.
+ *   q, o : [B, H, D] fp16        k, v : [B, KVH, L, D] fp16
+ *   head h reads KV head h / (H / KVH); H / KVH <= 16; D == 128.
+ *   o = softmax(q k^T * sm_scale) v, fp32 softmax and accumulation.
+ */
+int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o,
+                       int dtype, int64_t B, int32_t H, int32_t KVH, int64_t L,
+                       int32_t D, float sm_scale, void* ws, size_t ws_bytes,
+                       void* stream);
+
+/*
+ * StreamingLLM sink + window decode over a compacted [B, KVH, sink+window, D]
+ * fp16 cache.  Replaces sparse_kernel.py:105-118 (sparse_decode_attention) and
+ * sparse_kernel.py:67-102; slot validity follows _kv_indices
+ * (sparse_kernel.py:15-46) for KVDEC_LAYOUT_LINEAR.
+ */
+int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
+                        void* o, int dtype, int64_t B, int32_t H, int32_t KVH,
+                        int64_t seq_len, int32_t window, int32_t sink,
+                        int32_t layout, float sm_scale, void* ws,
+                        size_t ws_bytes, void* stream);
+
+/*
+ * KIVI per-channel quantization of K.  Replaces quant_kernel.py:106-126
+ * (quantize_k_cache) and quant_kernel.py:44-103.
+ *   x      : [B, KVH, N, D] of in_dtype (KVDEC_F32, KVDEC_F16 or KVDEC_BF16)
+ *   packed : [B, KVH, N/4, D] u8, code of token 4p+j in bits 2j..2j+1
+ *   scale, zero : [B, KVH, N/group, D] fp16
+ *   N % group == 0, D even, group == 32, bits == 2.
+ * Codes are bit-exact to the IEEE-float32 closed form.
+ */
+int kvdec_quantize_k(const void* x, int in_dtype, void* packed_u8,
+                     void* scale_f16, void* zero_f16, int64_t B, int32_t KVH,
+                     int64_t N, int32_t D, int32_t group, int32_t bits,
+                     void* stream);
+
+/*
+ * KIVI per-token quantization of V.  Replaces quant_kernel.py:193-214
+ * (quantize_v_cache) and quant_kernel.py:129-190.
+ *   packed : [B, KVH, N, D/4] u8, code of channel 4c+j in bits 2j..2j+1
+ *   scale, zero : [B, KVH, N, D/group] fp16
+ *   D % group == 0, group == 32, bits == 2.
+ */
+int kvdec_quantize_v(const void* x, int in_dtype, void* packed_u8,
+                     void* scale_f16, void* zero_f16, int64_t B, int32_t KVH,
+                     int64_t N, int32_t D, int32_t group, int32_t bits,
+                     void* stream);
+
+/*
+ * Fused sink + window + KIVI-2bit decode.  Replaces quant_kernel.py:551-581
+ * (sparse_decode_attention_quantized) and quant_kernel.py:436-548.
+ *   k_res, v_res : [B, KVH, residual, D] fp16 (the most recent tokens)
+ *   kivi[12] (host array of device pointers), in this order:
+ *     k_sink_packed [B,KVH,group/4,D] u8, k_sink_scale, k_sink_zero [B,KVH,1,D],
+ *     v_sink_packed [B,KVH,group,D/4] u8, v_sink_scale, v_sink_zero [B,KVH,group,D/group],
+ *     k_win_packed  [B,KVH,(W-R)/4,D],   k_win_scale,  k_win_zero  [B,KVH,(W-R)/group,D],
+ *     v_win_packed  [B,KVH,W-R,D/4],     v_win_scale,  v_win_zero  [B,KVH,W-R,D/group]
+ *   (the k_win / v_win pointers may be NULL when window == residual).
+ *   Slot s of the logical [sink + window] cache is sink token s (s < sink),
+ *   window-old token s - sink, or residual row s - (sink + window - residual);
+ *   slots are masked by _kv_indices validity.  window >= residual,
+ *   (window - residual) % group == 0, residual % 32 == 0, sink <= group.
+ */
+int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res,
+                             const void* const* kivi, void* o, int64_t B,
+                             int32_t H, int32_t KVH, int64_t seq_len,
+                             int32_t window, int32_t sink, int32_t residual,
+                             int32_t group, int32_t bits, float sm_scale,
+                             void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Dequantize one block_n-token tile of a K region, with the reference's
+ * clamping: byte = clamp(tok_start/4 + t/4, 0, num_packed-1) (C division),
+ * code = (byte >> 2*(t%4)) & 3, group = min(byte/(group/4), num_groups-1),
+ * out = float(scale) * (code - float(zero)).  Replaces the debug wrapper
+ * test_dequantize_tile_isolated.py:28-44 around quant_kernel.py:219-266.
+ *   packed [B,KVH,num_packed,D] u8, scale/zero [B,KVH,num_groups,D] fp16,
+ *   out [B,KVH,block_n,D] fp32.
+ */
+int kvdec_dequant_k_tile(const void* packed, const void* scale,
+                         const void* zero, void* out_f32, int64_t tok_start,
+                         int64_t num_packed, int64_t num_groups, int32_t B,
+                         int32_t KVH, int32_t D, int32_t block_n,
+                         void* stream);
+
+/*
+ * Dequantize one block_n-token tile of a V region: token =
+ * clamp(tok_start + t, 0, seq_len-1), code from byte d/4 shifted 2*(d%4),
+ * group d/32.  Replaces test_dequantize_tile_isolated.py:47-63 around
+ * quant_kernel.py:269-311.
+ *   packed [B,KVH,seq_len,D/4] u8, scale/zero [B,KVH,seq_len,D/32] fp16,
+ *   out [B,KVH,block_n,D] fp32.
+ */
+int kvdec_dequant_v_tile(const void* packed, const void* scale,
+                         const void* zero, void* out_f32, int64_t tok_start,
+                         int64_t seq_len, int32_t B, int32_t KVH, int32_t D,
+                         int32_t block_n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVDEC_H_ */

@@ -1,0 +1,104 @@
+"""ctypes binding of libkvdec.so (the C ABI in include/kvdec.h).
+
+The library is loaded from this directory; there is no fallback: importing a
+wrapper module when the library has not been built raises ImportError with the
+build command.  Negative return codes (host-side validation) become
+ValueError, positive ones (HIP launch errors) RuntimeError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libkvdec.so")
+
+# element types / layouts / workspace kinds (include/kvdec.h)
+F16, F32, BF16 = 0, 1, 2
+LAYOUT_LINEAR, LAYOUT_RING = 0, 1
+KIND_DENSE, KIND_SPARSE, KIND_KIVI = 0, 1, 2
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); every symbol include/kvdec.h declares
+SIGNATURES = {
+    "kvdec_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "kvdec_version": (ctypes.c_char_p, []),
+    "kvdec_num_splits": (ctypes.c_int, [ctypes.c_int, _i64, _i32, _i64]),
+    "kvdec_workspace_bytes": (_sz, [ctypes.c_int, _i64, _i32, _i32, _i64, _i32]),
+    "kvdec_dense_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32, _i64,
+                                          _i32, _f32, _vp, _sz, _vp]),
+    "kvdec_sparse_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32, _i64,
+                                           _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
+    "kvdec_quantize_k": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _vp, _vp, _i64, _i32, _i64, _i32,
+                                        _i32, _i32, _vp]),
+    "kvdec_quantize_v": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _vp, _vp, _i64, _i32, _i64, _i32,
+                                        _i32, _i32, _vp]),
+    "kvdec_sparse_decode_kivi": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _i64, _i32,
+                                                _i32, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _vp,
+                                                _sz, _vp]),
+    "kvdec_dequant_k_tile": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32,
+                                            _i32, _vp]),
+    "kvdec_dequant_v_tile": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32,
+                                            _vp]),
+}
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python {os.path.join(_HERE, 'build.py')}` "
+            "(or __graft_entry__.build()); there is no CPU fallback")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+class KvdecLaunchError(RuntimeError):
+    """A HIP launch inside libkvdec failed (positive return code)."""
+
+
+def strerror(code: int) -> str:
+    return lib.kvdec_strerror(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    if code == 0:
+        return
+    msg = f"{what}: {strerror(code)} (kvdec code {code})"
+    if code < 0:
+        raise ValueError(msg)
+    raise KvdecLaunchError(msg)
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t) -> int | None:
+    """hipStream_t of torch's current stream on t's device."""
+    import torch
+    if t is None or not t.is_cuda:
+        return None
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def workspace(kind: int, B: int, H: int, KVH: int, n_slots: int, D: int, device):
+    """Split-K workspace for one call (None when a single pass suffices)."""
+    import torch
+    nbytes = lib.kvdec_workspace_bytes(kind, B, H, KVH, n_slots, D)
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes

@@ -1,0 +1,49 @@
+"""StreamingLLM sink + sliding-window decode attention on MI355X (gfx950).
+
+Drop-in for the reference's sparse_kernel.py.  The compacted cache holds
+``sink + window`` slots per (batch, KV head); in the reference's linear
+layout slot s < sink holds position s and slot sink + i holds position
+(seq_len - window) + i, and a slot is attended only while that position
+exists (the _kv_indices rule, sparse_kernel.py:15-46).  layout="ring" selects
+the ring-buffer layout (position p >= sink in slot sink + (p - sink) % window)
+used by a streaming writer; both give the same result in steady state.
+"""
+
+import torch
+
+from constants import D_HEAD, SINK_SIZE
+import _checks
+import _kvdec as K
+
+_LAYOUTS = {"linear": K.LAYOUT_LINEAR, "ring": K.LAYOUT_RING}
+
+
+def sparse_decode_attention(q, k_cache, v_cache, seq_len, window, sink=SINK_SIZE, sm_scale=None,
+                            layout="linear"):
+    """k_cache/v_cache must be [BATCH, N_KV_HEADS, SINK+WINDOW, D_HEAD].
+
+    Mirrors sparse_kernel.py:105-118 (same arguments and defaults; ``layout``
+    is an added keyword).  fp16, contiguous, D_HEAD == 128.
+    """
+    _checks.require_gpu_tensor("q", q, ndim=3)
+    _checks.require_gpu_tensor("k_cache", k_cache, ndim=4)
+    _checks.require_gpu_tensor("v_cache", v_cache, ndim=4)
+    _checks.require_same_device(("q", q), ("k_cache", k_cache), ("v_cache", v_cache))
+    if layout not in _LAYOUTS:
+        raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {layout!r}")
+    B, H, D = q.shape
+    KVH = k_cache.shape[1]
+    window, sink, seq_len = int(window), int(sink), int(seq_len)
+    if window < 0 or sink < 0:
+        raise ValueError(f"window and sink must be >= 0 (window={window}, sink={sink})")
+    _checks.require_shape("k_cache", k_cache, (B, KVH, sink + window, D))
+    _checks.require_shape("v_cache", v_cache, (B, KVH, sink + window, D))
+    o = torch.empty_like(q)
+    if sm_scale is None:
+        sm_scale = D_HEAD**-0.5
+    ws, nbytes = K.workspace(K.KIND_SPARSE, B, H, KVH, sink + window, D, q.device)
+    rc = K.lib.kvdec_sparse_decode(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), K.ptr(o), K.F16, B, H,
+                                   KVH, seq_len, window, sink, _LAYOUTS[layout], float(sm_scale),
+                                   K.ptr(ws), nbytes, K.stream_of(q))
+    K.check(rc, "sparse_decode_attention")
+    return o

@@ -1,0 +1,195 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/kvdec.h declares, and rejects bad arguments with the documented
+negative codes before any HIP call."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+import _kvdec as K
+
+HEADER = os.path.join(ROOT, "include", "kvdec.h")
+FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+
+E = {
+    "NULL": -1, "SHAPE": -2, "DTYPE": -3, "GROUP": -4, "DGROUP": -5, "WORKSPACE": -6,
+    "WINDOW": -7, "SEQLEN": -8, "BITS": -9, "UNSUPPORTED": -10,
+}
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t)\s+(kvdec_\w+)\s*\(", text, re.M)))
+
+
+def _header_codes():
+    text = open(HEADER).read()
+    return {m.group(1): int(m.group(2)) for m in re.finditer(r"#define KVDEC_E_(\w+) \((-\d+)\)", text)}
+
+
+def test_header_and_binding_agree():
+    funcs = _header_functions()
+    assert len(funcs) == 11
+    assert funcs == sorted(K.SIGNATURES)
+    assert _header_codes() == E
+
+
+def test_library_exports_every_symbol():
+    lib = ctypes.CDLL(K.LIB_PATH)
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_strerror_and_version():
+    assert K.strerror(0) == "success"
+    for code in E.values():
+        assert K.strerror(code) and "unknown" not in K.strerror(code)
+    assert K.strerror(-999) == "unknown kvdec error"
+    assert K.lib.kvdec_version().decode().startswith("kvdec")
+    # the reference's assert messages are kept verbatim
+    assert K.strerror(E["GROUP"]) == "this simple version assumes seq_len is a multiple of group_size"
+    assert K.strerror(E["DGROUP"]) == "this simple version assumes D_HEAD is a multiple of group_size"
+
+
+def test_split_plan_and_workspace_arithmetic():
+    # the metric configuration: dense over 163840 tokens splits, sparse/KIVI W=256 do not
+    s_dense = K.lib.kvdec_num_splits(K.KIND_DENSE, 32, 8, 163840)
+    assert s_dense > 1
+    assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 32, 64, 8, 163840, 128) == 256 * s_dense * 8 * 130 * 4
+    assert K.lib.kvdec_num_splits(K.KIND_SPARSE, 32, 8, 260) == 1
+    assert K.lib.kvdec_workspace_bytes(K.KIND_SPARSE, 32, 64, 8, 260, 128) == 0
+    assert K.lib.kvdec_num_splits(K.KIND_KIVI, 32, 8, 256) == 1
+    assert K.lib.kvdec_workspace_bytes(K.KIND_KIVI, 32, 64, 8, 256, 128) == 0
+    # every split keeps at least 4 tiles per wave
+    for L in (1, 2, 100, 8192, 32768, 131072, 163840):
+        s = K.lib.kvdec_num_splits(K.KIND_DENSE, 32, 8, L)
+        tiles = -(-L // 32)
+        assert s == 1 or tiles / s >= 16
+    # invalid heads -> no workspace
+    assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 32, 64, 7, 1000, 128) == 0
+    assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 32, 64, 8, 1000, 64) == 0
+
+
+def _dense(**kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, dtype=K.F16, B=32, H=64, KVH=8, L=1024, D=128,
+             scale=0.088, ws=None, wsb=0, stream=None)
+    a.update(kw)
+    return K.lib.kvdec_dense_decode(a["q"], a["k"], a["v"], a["o"], a["dtype"], a["B"], a["H"],
+                                    a["KVH"], a["L"], a["D"], a["scale"], a["ws"], a["wsb"],
+                                    a["stream"])
+
+
+def test_dense_validation():
+    assert _dense(q=None) == E["NULL"]
+    assert _dense(o=None) == E["NULL"]
+    assert _dense(dtype=K.F32) == E["DTYPE"]
+    assert _dense(KVH=7) == E["SHAPE"]            # H % KVH != 0
+    assert _dense(H=8 * 32, KVH=8) == E["SHAPE"]  # group of 32 > 16 MFMA columns
+    assert _dense(D=64) == E["SHAPE"]
+    assert _dense(B=0) == E["SHAPE"]
+    assert _dense(L=0) == E["SEQLEN"]
+    assert _dense(L=1 << 23) == E["SHAPE"]        # 32-bit in-head offsets
+    assert _dense(L=163840) == E["WORKSPACE"]     # needs split-K workspace
+    assert _dense(L=163840, ws=FAKE, wsb=16) == E["WORKSPACE"]
+
+
+def _sparse(**kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, dtype=K.F16, B=32, H=64, KVH=8, seq_len=5000, W=256,
+             S=4, layout=0, scale=0.088, ws=None, wsb=0, stream=None)
+    a.update(kw)
+    return K.lib.kvdec_sparse_decode(a["q"], a["k"], a["v"], a["o"], a["dtype"], a["B"], a["H"],
+                                     a["KVH"], a["seq_len"], a["W"], a["S"], a["layout"],
+                                     a["scale"], a["ws"], a["wsb"], a["stream"])
+
+
+def test_sparse_validation():
+    assert _sparse(v=None) == E["NULL"]
+    assert _sparse(dtype=K.BF16) == E["DTYPE"]
+    assert _sparse(seq_len=0) == E["SEQLEN"]
+    assert _sparse(W=-1) == E["WINDOW"]
+    assert _sparse(S=-1) == E["WINDOW"]
+    assert _sparse(W=0, S=0) == E["WINDOW"]
+    assert _sparse(layout=2) == E["UNSUPPORTED"]
+    assert _sparse(layout=1, W=0) == E["WINDOW"]
+    assert _sparse(W=16384) == E["WORKSPACE"]
+
+
+def _kivi(ptrs=None, **kw):
+    a = dict(q=FAKE, kr=FAKE, vr=FAKE, o=FAKE, B=32, H=64, KVH=8, seq_len=200000, W=256, S=4, R=128,
+             group=32, bits=2, scale=0.088, ws=None, wsb=0, stream=None)
+    a.update(kw)
+    arr = (K._vp * 12)(*([0x1000] * 12 if ptrs is None else ptrs))
+    return K.lib.kvdec_sparse_decode_kivi(a["q"], a["kr"], a["vr"], arr, a["o"], a["B"], a["H"],
+                                          a["KVH"], a["seq_len"], a["W"], a["S"], a["R"],
+                                          a["group"], a["bits"], a["scale"], a["ws"], a["wsb"],
+                                          a["stream"])
+
+
+def test_kivi_validation():
+    assert _kivi(q=None) == E["NULL"]
+    assert _kivi(ptrs=[0x1000] * 5 + [None] + [0x1000] * 6) == E["NULL"]
+    assert _kivi(ptrs=[0x1000] * 6 + [None] * 6) == E["NULL"]          # window-old needed at W=256
+    assert _kivi(bits=4) == E["BITS"]
+    assert _kivi(group=64) == E["UNSUPPORTED"]
+    assert _kivi(W=64) == E["WINDOW"]                                 # W < residual
+    assert _kivi(S=0) == E["WINDOW"]
+    assert _kivi(S=33) == E["WINDOW"]
+    assert _kivi(R=100) == E["WINDOW"]
+    assert _kivi(W=128 + 48) == E["GROUP"]                            # window-old not whole groups
+    assert _kivi(seq_len=0) == E["SEQLEN"]
+    assert _kivi(KVH=3) == E["SHAPE"]
+    assert _kivi(W=8192) == E["WORKSPACE"]
+
+
+def _quant(fn, **kw):
+    a = dict(x=FAKE, dt=K.F32, p=FAKE, s=FAKE, z=FAKE, B=1, KVH=8, N=256, D=128, group=32, bits=2,
+             stream=None)
+    a.update(kw)
+    return fn(a["x"], a["dt"], a["p"], a["s"], a["z"], a["B"], a["KVH"], a["N"], a["D"], a["group"],
+              a["bits"], a["stream"])
+
+
+@pytest.mark.parametrize("name", ["kvdec_quantize_k", "kvdec_quantize_v"])
+def test_quantize_validation(name):
+    fn = getattr(K.lib, name)
+    assert _quant(fn, x=None) == E["NULL"]
+    assert _quant(fn, z=None) == E["NULL"]
+    assert _quant(fn, bits=4) == E["BITS"]
+    assert _quant(fn, dt=7) == E["DTYPE"]
+    assert _quant(fn, N=0) == E["SHAPE"]
+    assert _quant(fn, group=64) == E["UNSUPPORTED"]
+    if name == "kvdec_quantize_k":
+        assert _quant(fn, N=100) == E["GROUP"]
+        assert _quant(fn, D=7) == E["SHAPE"]
+    else:
+        assert _quant(fn, D=100) == E["DGROUP"]
+
+
+def test_dequant_tile_validation():
+    assert K.lib.kvdec_dequant_k_tile(None, FAKE, FAKE, FAKE, 0, 8, 1, 1, 1, 128, 128, None) == E["NULL"]
+    assert K.lib.kvdec_dequant_k_tile(FAKE, FAKE, FAKE, FAKE, 0, 0, 1, 1, 1, 128, 128, None) == E["SHAPE"]
+    assert K.lib.kvdec_dequant_v_tile(FAKE, FAKE, FAKE, FAKE, 0, 0, 1, 1, 128, 128, None) == E["SHAPE"]
+    assert K.lib.kvdec_dequant_v_tile(FAKE, FAKE, FAKE, FAKE, 0, 32, 1, 1, 100, 128, None) == E["DGROUP"]
+
+
+def test_python_wrappers_reject_cpu_tensors():
+    import torch
+    import dense_kernel
+    import quant_kernel
+    import sparse_kernel
+    q = torch.zeros(2, 16, 128, dtype=torch.float16)
+    k = torch.zeros(2, 2, 8, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        dense_kernel.dense_decode_attention(q, k, k, seq_len=8)
+    with pytest.raises(ValueError, match="GPU"):
+        sparse_kernel.sparse_decode_attention(q, k, k, seq_len=8, window=4)
+    with pytest.raises(ValueError, match="GPU"):
+        quant_kernel.quantize_k_cache(torch.zeros(1, 1, 32, 128))
+    with pytest.raises(AssertionError, match="multiple of group_size"):
+        quant_kernel.quantize_k_cache(torch.zeros(1, 1, 33, 128))
+    with pytest.raises(AssertionError, match="multiple of group_size"):
+        quant_kernel.quantize_v_cache(torch.zeros(1, 1, 32, 100))

@@ -1,0 +1,96 @@
+"""Dense GQA decode on the GPU vs the CPU oracle (restates the intent of the
+reference's test_dense_correctness.py with a tighter gate)."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+from helpers import ATTN_TOL, REF_TOL, SCALE, dev, host, max_abs, randn, say
+from oracle import kvdec_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q16, k16, v16, device, L=None, scale=None):
+    from dense_kernel import dense_decode_attention
+    L = k16.shape[2] if L is None else L
+    o = dense_decode_attention(dev(q16, device), dev(k16, device), dev(v16, device), seq_len=L,
+                               sm_scale=scale)
+    torch.cuda.synchronize()
+    return host(o)
+
+
+def test_dense_golden(device):
+    g = load_golden("dense_golden.npz")
+    say("dense golden")
+    o = _run(g["q"], g["k"], g["v"], device)
+    assert max_abs(o, g["o"]) < ATTN_TOL
+
+
+@pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 100, 1000, 4097, 8192])
+def test_dense_lengths(L, device):
+    B, H, KVH, D = 4, 64, 8, 128
+    q = randn((B, H, D), L)
+    k = randn((B, KVH, L, D), L + 1)
+    v = randn((B, KVH, L, D), L + 2)
+    q16, k16, v16 = q.astype(np.float16), k.astype(np.float16), v.astype(np.float16)
+    say(f"dense B={B} L={L}")
+    o = _run(q16, k16, v16, device)
+    assert o.dtype == np.float16
+    assert max_abs(o, O.dense_attention(q16, k16, v16, SCALE)) < ATTN_TOL
+    # the reference's own gate: fp16 kernel vs fp32 originals
+    assert max_abs(o, O.dense_attention(q, k, v, SCALE, dtype=np.float32)) < REF_TOL
+
+
+@pytest.mark.parametrize("H,KVH", [(16, 16), (32, 2), (48, 4), (64, 8)])
+def test_dense_group_sizes(H, KVH, device):
+    B, L, D = 3, 700, 128
+    q16 = randn((B, H, D), 5, np.float16)
+    k16 = randn((B, KVH, L, D), 6, np.float16)
+    v16 = randn((B, KVH, L, D), 7, np.float16)
+    say(f"dense H={H} KVH={KVH}")
+    o = _run(q16, k16, v16, device, scale=0.05)
+    assert max_abs(o, O.dense_attention(q16, k16, v16, 0.05)) < ATTN_TOL
+
+
+def test_dense_peaked_softmax(device):
+    """Large logits (scaled keys): the online max/rescale path."""
+    B, H, KVH, L, D = 2, 64, 8, 3000, 128
+    q16 = (randn((B, H, D), 8) * 3).astype(np.float16)
+    k16 = (randn((B, KVH, L, D), 9) * 3).astype(np.float16)
+    v16 = randn((B, KVH, L, D), 10, np.float16)
+    say("dense peaked")
+    o = _run(q16, k16, v16, device)
+    assert max_abs(o, O.dense_attention(q16, k16, v16, SCALE)) < ATTN_TOL
+
+
+def test_dense_long_context_large_offsets(device):
+    """The reference's 131072 case at full batch: per-(b, kv) offsets run far
+    past 2^31 elements; rows b=0 and b=31 are checked against the oracle."""
+    B, H, KVH, L, D = 32, 64, 8, 131072, 128
+    gen = torch.Generator(device=device).manual_seed(0)
+    say("dense B=32 L=131072 (generate)")
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    k = torch.randn(B, KVH, L, D, generator=gen, device=device, dtype=torch.float16)
+    v = torch.randn(B, KVH, L, D, generator=gen, device=device, dtype=torch.float16)
+    from dense_kernel import dense_decode_attention
+    say("dense B=32 L=131072 (run)")
+    o = host(dense_decode_attention(q, k, v, seq_len=L))
+    torch.cuda.synchronize()
+    for b in (0, 31):
+        ref = O.dense_attention(host(q[b:b + 1]), host(k[b:b + 1]), host(v[b:b + 1]), SCALE)
+        assert max_abs(o[b:b + 1], ref) < ATTN_TOL, b
+    del k, v
+
+
+def test_dense_rejects_bad_shapes(device):
+    from dense_kernel import dense_decode_attention
+    q = torch.zeros(2, 64, 128, dtype=torch.float16, device=device)
+    k = torch.zeros(2, 8, 10, 128, dtype=torch.float16, device=device)
+    with pytest.raises(ValueError):
+        dense_decode_attention(q, k, k, seq_len=11)
+    with pytest.raises(ValueError):
+        dense_decode_attention(q.float(), k, k, seq_len=10)
+    with pytest.raises(ValueError):
+        dense_decode_attention(q, k[:, :7], k[:, :7], seq_len=10)

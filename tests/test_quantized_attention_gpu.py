@@ -1,0 +1,119 @@
+"""Fused sink + window + KIVI-2bit decode on the GPU vs the CPU oracle
+(restates the reference's test_quantized_attention_correctness.py, adds W=R,
+the split-K windows, ramp-up and the cache builder's bit-exact codes)."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+from helpers import ATTN_TOL, REF_TOL, SCALE, dev, host, max_abs, randn, say
+from oracle import kvdec_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+S, R = 4, 128
+
+
+def _attend(q, cache, L, W, device=None):
+    from quant_kernel import sparse_decode_attention_quantized
+    c = cache
+    o = sparse_decode_attention_quantized(
+        q, c["k_residual"], c["v_residual"],
+        c["k_sink_packed"], c["k_sink_scale"], c["k_sink_zero"],
+        c["v_sink_packed"], c["v_sink_scale"], c["v_sink_zero"],
+        c["k_win_packed"], c["k_win_scale"], c["k_win_zero"],
+        c["v_win_packed"], c["v_win_scale"], c["v_win_zero"],
+        seq_len=L, window=W)
+    torch.cuda.synchronize()
+    return host(o)
+
+
+def _host_cache(cache):
+    return {k: host(v) for k, v in cache.items()}
+
+
+def test_kivi_golden(device):
+    g = load_golden("kivi_golden.npz")
+    W = int(g["window"])
+    from quant_kernel import build_quantized_kv_cache
+    say("kivi golden build")
+    cache = build_quantized_kv_cache(dev(g["k_compacted"], device), dev(g["v_compacted"], device))
+    hc = _host_cache(cache)
+    for key in O.CACHE_KEYS:
+        np.testing.assert_array_equal(hc[key], g["cache_" + key], err_msg=key)
+    q = dev(g["q"], device)
+    say("kivi golden attend")
+    assert max_abs(_attend(q, cache, S + W + 1000, W), g["o_steady"]) < ATTN_TOL
+    assert max_abs(_attend(q, cache, 150, W), g["o_ramp"]) < ATTN_TOL
+
+
+@pytest.mark.parametrize("W", [128, 256, 512, 1024, 4096, 8192])
+def test_quantized_attention_steady_state(W, device):
+    """Reference case (seed 3 analogue, W in {256, 512, 8192}) plus W = R and
+    the split-K windows; q and the compacted cache are fp16 N(0,1)."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D = 32, 64, 8, 128
+    L = S + W + 1000
+    gen = torch.Generator(device=device).manual_seed(3 + W)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    say(f"kivi steady W={W}")
+    cache = build_quantized_kv_cache(kc, vc)
+    o = _attend(q, cache, L, W)
+    hc = _host_cache(cache)
+    qh = host(q)
+    # codes built on the GPU equal the oracle's build on the same fp16 cache
+    oc = O.build_quantized_kv_cache(host(kc), host(vc))
+    for key in O.CACHE_KEYS:
+        np.testing.assert_array_equal(hc[key], oc[key], err_msg=key)
+    ref = O.quantized_attention(qh, W - R, hc, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+    assert max_abs(o, O.quantized_attention(qh, W - R, hc, SCALE, dtype=np.float32)) < REF_TOL
+
+
+def test_quantized_attention_outlier_keys(device):
+    """Config-5 distributions: K with 4 channels x10 (sharper softmax)."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D, W = 32, 64, 8, 128, 256
+    gen = torch.Generator(device=device).manual_seed(11)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    outl = torch.randperm(D, generator=torch.Generator().manual_seed(0))[:4].tolist()
+    kc[..., outl] *= 10
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    say("kivi outliers")
+    cache = build_quantized_kv_cache(kc, vc)
+    o = _attend(q, cache, 163840, W)
+    ref = O.quantized_attention(host(q), W - R, _host_cache(cache), SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+
+
+@pytest.mark.parametrize("L", [1, 3, 4, 5, 60, 200, 300, 387, 388, 389])
+def test_quantized_attention_rampup(L, device):
+    """Ramp-up (seq_len <= S + W): only the slots the _kv_indices rule marks
+    valid are attended.  Unwritten slots hold 3.0 before quantization: far
+    enough from N(0,1) data that a leak moves the output, small enough that
+    the quantization groups they share with real tokens stay well conditioned
+    (1e4, as in the fp16 sparse test, would swamp those groups' scales)."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D, W = 2, 16, 2, 128, 384
+    kf = randn((B, KVH, max(L, 1), D), 30 + L)
+    vf = randn((B, KVH, max(L, 1), D), 31 + L)
+    kc, vc = O.build_compacted_cache(kf, vf, L, W, S, garbage=3.0)
+    q16 = randn((B, H, D), 32 + L, np.float16)
+    say(f"kivi ramp L={L}")
+    cache = build_quantized_kv_cache(dev(kc.astype(np.float16), device), dev(vc.astype(np.float16), device))
+    o = _attend(dev(q16, device), cache, L, W)
+    ref = O.quantized_attention_masked(q16, _host_cache(cache), L, W, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+
+
+def test_quantized_attention_rejects_small_window(device):
+    from quant_kernel import build_quantized_kv_cache
+    kc = torch.zeros(1, 2, S + 256, 128, dtype=torch.float16, device=device)
+    cache = build_quantized_kv_cache(kc, kc)
+    q = torch.zeros(1, 16, 128, dtype=torch.float16, device=device)
+    with pytest.raises(ValueError):
+        _attend(q, cache, 1000, 64)
