@@ -11,6 +11,12 @@ from __future__ import annotations
 import ctypes
 import os
 
+# torch must load its bundled HIP runtime before libkvdec.so is opened: both
+# carry the SONAME libamdhip64.so.7, and whichever is loaded first is the one
+# the dynamic loader binds libkvdec to.  Opening libkvdec first would pull the
+# system runtime in beside torch's and leave two HIP runtimes in one process.
+import torch  # noqa: F401
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkvdec.so")
 
