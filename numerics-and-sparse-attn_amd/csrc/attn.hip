@@ -2,17 +2,16 @@
 // sink+window decode and the fused KIVI-2bit decode, plus their C-ABI entry
 // points (declared in include/kvdec.h).
 //
-// One workgroup = 4 waves = one (KV head, split) work item.  Each wave streams
-// a contiguous run of 32-token tiles of that KV head through MFMA (all GQA
-// query heads of the KV head at once, so each K/V byte is read once), keeps an
-// online softmax, and the 4 waves merge through LDS.  With one split the
-// workgroup writes the fp16 output directly; otherwise it writes an fp32
-// partial (m, l, acc) and merge_kernel combines the splits.
+// One workgroup = one (KV head, split) work item of 4 or 8 waves.  Each wave
+// streams a contiguous run of 32-token tiles of that KV head through MFMA
+// (all GQA query heads of the KV head at once, so each K/V byte is read
+// once), keeps an online softmax, and the waves merge through LDS.  With one
+// split the workgroup writes the fp16 output directly; otherwise it writes an
+// fp32 partial (m, l, acc) and merge_kernel combines the splits.  At the
+// benchmark shapes (B*KVH = 256 KV heads) every path runs in one pass.
 
 #include "kvdec_device.h"
 #include "kvdec.h"
-
-#include <string.h>
 
 using namespace kvdec;
 
@@ -43,43 +42,55 @@ __device__ __forceinline__ void load_q_operand(const AttnCommon& P, int64_t b, i
   }
 }
 
-// Merge the 4 waves of the workgroup and emit the output or a partial.
-__device__ __forceinline__ void finish_block(const AttnCommon& P, WaveState& st, int64_t pair,
-                                             int split, int lane, int wave) {
-  __shared__ float sh_m[kWaves][kMaxGroup];
-  __shared__ float sh_l[kWaves][kMaxGroup];
-  __shared__ float sh_o[kWaves][kMaxGroup][kHeadDim + 4];
+// LDS of a workgroup: the per-wave KIVI staging slots (quantized sources
+// only), then the merge area -- per wave, the max and sum of 16 heads and the
+// G x 128 partial outputs (rows padded by 4 floats).
+constexpr int kORow = kHeadDim + 4;
+__host__ __device__ constexpr size_t merge_lds_bytes(int nw, int G) {
+  return (size_t)(2 * nw * kMaxGroup + nw * G * kORow) * sizeof(float);
+}
+__host__ __device__ constexpr size_t stage_lds_bytes(int nw, bool quant) {
+  return quant ? (size_t)nw * kQSlotBytes : 0;
+}
+
+// Merge the NW waves of the workgroup and emit the output or a partial.
+template <int NW>
+__device__ __forceinline__ void finish_block(const AttnCommon& P, WaveState& st, float* smem,
+                                             int64_t pair, int split, int lane, int wave) {
+  float* sh_m = smem;                       // [NW][16]
+  float* sh_l = smem + NW * kMaxGroup;      // [NW][16]
+  float* sh_o = smem + 2 * NW * kMaxGroup;  // [NW][G][kORow]
 
   st.l += __shfl_xor(st.l, 16);
   st.l += __shfl_xor(st.l, 32);
   const int n = lane & 15, g = lane >> 4;
   if (n < P.G) {
     if (g == 0) {
-      sh_m[wave][n] = st.m;
-      sh_l[wave][n] = st.l;
+      sh_m[wave * kMaxGroup + n] = st.m;
+      sh_l[wave * kMaxGroup + n] = st.l;
     }
+    float* orow = sh_o + ((size_t)wave * P.G + n) * kORow + 32 * g;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) sh_o[wave][n][32 * g + 8 * r + jj] = st.O[jj][r];
+      for (int jj = 0; jj < 8; ++jj) orow[8 * r + jj] = st.O[jj][r];
   }
   __syncthreads();
 
   const int64_t b = pair / P.KVH;
   const int kvh = (int)(pair % P.KVH);
   const size_t total = (size_t)P.pairs * P.n_splits * P.G;
-  for (int e = threadIdx.x; e < P.G * kHeadDim; e += kBlock) {
+  for (int e = threadIdx.x; e < P.G * kHeadDim; e += 64 * NW) {
     const int hn = e / kHeadDim, d = e % kHeadDim;
-    float M = -INFINITY;
+    float M = kMaxSentinel;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sh_m[w][hn]);
-    const float Mu = (M == -INFINITY) ? 0.f : M;
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sh_m[w * kMaxGroup + hn]);
     float L = 0.f, acc = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = __builtin_amdgcn_exp2f(sh_m[w][hn] - Mu);
-      L += sh_l[w][hn] * f;
-      acc += sh_o[w][hn][d] * f;
+    for (int w = 0; w < NW; ++w) {
+      const float f = __builtin_amdgcn_exp2f(sh_m[w * kMaxGroup + hn] - M);
+      L += sh_l[w * kMaxGroup + hn] * f;
+      acc += sh_o[((size_t)w * P.G + hn) * kORow + d] * f;
     }
     if (P.n_splits == 1) {
       P.o[((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + d] = (_Float16)(acc / L);
@@ -95,10 +106,11 @@ __device__ __forceinline__ void finish_block(const AttnCommon& P, WaveState& st,
 }
 
 // Stream fp16 tiles [tb, te) of one region through the wave, two tiles in
-// flight (ping-pong register buffers).
+// flight (ping-pong register buffers).  Row r of the region is slot
+// slot_base + r.
 __device__ __forceinline__ void run_f16_tiles(const _Float16* __restrict__ kb,
                                               const _Float16* __restrict__ vb, int rows,
-                                              int64_t slot_base, int tb, int te,
+                                              int slot_base, int tb, int te,
                                               const half8 (&qB)[4], const AttnCommon& P,
                                               WaveState& st, int lane) {
   if (tb >= te) return;
@@ -106,21 +118,22 @@ __device__ __forceinline__ void run_f16_tiles(const _Float16* __restrict__ kb,
   load_f16_tile(kb, vb, kTile * tb, rows, lane, A);
   for (int ti = tb; ti < te; ti += 2) {
     if (ti + 1 < te) load_f16_tile(kb, vb, kTile * (ti + 1), rows, lane, B);
-    tile_step(A, qB, slot_base + (int64_t)kTile * ti, kTile, P.R, P.scale_log2, st, lane);
+    tile_step(A, qB, slot_base + kTile * ti, P.R, P.scale_log2, st, lane);
     if (ti + 1 >= te) break;
     if (ti + 2 < te) load_f16_tile(kb, vb, kTile * (ti + 2), rows, lane, A);
-    tile_step(B, qB, slot_base + (int64_t)kTile * (ti + 1), kTile, P.R, P.scale_log2, st, lane);
+    tile_step(B, qB, slot_base + kTile * (ti + 1), P.R, P.scale_log2, st, lane);
   }
 }
 
 // fp16 rows: the dense cache [B, KVH, L, 128] or the compacted sparse cache
 // [B, KVH, sink+window, 128]; slot == row.
 struct F16Src {
+  static constexpr bool kQuant = false;
   const _Float16* k;
   const _Float16* v;
   int rows;
   __device__ __forceinline__ void run(int64_t pair, int wb, int we, const half8 (&qB)[4],
-                                      const AttnCommon& P, WaveState& st, int lane) const {
+                                      const AttnCommon& P, WaveState& st, char*, int lane) const {
     const size_t off = (size_t)pair * rows * kHeadDim;
     run_f16_tiles(k + off, v + off, rows, 0, wb, we, qB, P, st, lane);
   }
@@ -129,6 +142,8 @@ struct F16Src {
 // KIVI cache: tile 0 = the sink group (quantized, `sink` real tokens), tiles
 // 1..nwt = window-old groups (quantized), then the fp16 residual tiles.
 struct KiviSrc {
+  static constexpr bool kQuant = true;
+  static constexpr int kRing = 3;   // quantized tiles in flight per wave
   const _Float16* kres;
   const _Float16* vres;
   int res_rows;
@@ -139,7 +154,8 @@ struct KiviSrc {
   int nwt;         // win_tok / 32
 
   __device__ __forceinline__ void run(int64_t pair, int wb, int we, const half8 (&qB)[4],
-                                      const AttnCommon& P, WaveState& st, int lane) const {
+                                      const AttnCommon& P, WaveState& st, char* slot,
+                                      int lane) const {
     const int nq = 1 + nwt;
     const int qb = wb, qe = we < nq ? we : nq;
     if (qb < qe) {
@@ -158,31 +174,44 @@ struct KiviSrc {
         W.vs += (size_t)pair * win_tok * 4;
         W.vz += (size_t)pair * win_tok * 4;
       }
-      RawQTile A, B;
-      Tile T;
-      load_q_tile(qb == 0 ? S : W, qb == 0 ? 0 : qb - 1, lane, A);
-      for (int ti = qb; ti < qe; ti += 2) {
-        if (ti + 1 < qe) load_q_tile(W, ti, lane, B);   // tile ti+1 >= 1: window-old tq = ti
-        decode_q_tile(A, lane, T);
-        tile_step(T, qB, ti == 0 ? 0 : sink + (int64_t)kTile * (ti - 1), ti == 0 ? sink : kTile,
-                  P.R, P.scale_log2, st, lane);
-        if (ti + 1 >= qe) break;
-        if (ti + 2 < qe) load_q_tile(W, ti + 1, lane, A);
-        decode_q_tile(B, lane, T);
-        tile_step(T, qB, sink + (int64_t)kTile * ti, kTile, P.R, P.scale_log2, st, lane);
+      // tile ti: 0 = sink group (slots 0..sink-1), else window-old group ti-1
+      auto load = [&](int ti, QTileRaw& X) {
+        if (ti == 0)
+          load_q_raw(S, 0, lane, X);
+        else
+          load_q_raw(W, ti - 1, lane, X);
+      };
+      // Ring of kRing raw tiles in flight; each is staged through the wave's
+      // LDS slot into operand layout just before it is consumed.
+      QTileRaw ring[kRing];
+#pragma unroll
+      for (int k = 0; k < kRing; ++k)
+        if (qb + k < qe) load(qb + k, ring[k]);
+      for (int base = qb; base < qe; base += kRing) {
+#pragma unroll
+        for (int k = 0; k < kRing; ++k) {
+          const int ti = base + k;
+          if (ti < qe) {
+            stage_q_raw(ring[k], slot, lane);
+            if (ti + kRing < qe) load(ti + kRing, ring[k]);
+            q_tile_step(slot, qB, ti == 0 ? 0 : sink + kTile * (ti - 1), ti == 0 ? sink : kTile,
+                        P.R, P.scale_log2, st, lane);
+          }
+        }
       }
     }
     const int fb = (wb > nq ? wb : nq) - nq, fe = we - nq;
     if (fb < fe) {
       const size_t off = (size_t)pair * res_rows * kHeadDim;
-      run_f16_tiles(kres + off, vres + off, res_rows, sink + (int64_t)win_tok, fb, fe, qB, P, st,
-                    lane);
+      run_f16_tiles(kres + off, vres + off, res_rows, sink + win_tok, fb, fe, qB, P, st, lane);
     }
   }
 };
 
-template <class Src>
-__global__ __launch_bounds__(kBlock) void attn_kernel(AttnCommon P, Src S) {
+// NW waves per workgroup, two waves per SIMD.
+template <class Src, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnCommon P, Src S) {
+  extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int split = (int)(blockIdx.x % (unsigned)P.n_splits);
   const int64_t pair = blockIdx.x / (unsigned)P.n_splits;
@@ -195,60 +224,73 @@ __global__ __launch_bounds__(kBlock) void attn_kernel(AttnCommon P, Src S) {
   const int t0 = split * P.tiles_per_split;
   const int t1 = min(t0 + P.tiles_per_split, P.n_tiles);
   const int nt = t1 - t0;
-  const int wb = t0 + (nt * wave) / kWaves;
-  const int we = t0 + (nt * (wave + 1)) / kWaves;
+  const int wb = t0 + (nt * wave) / NW;
+  const int we = t0 + (nt * (wave + 1)) / NW;
 
   WaveState st;
   wave_state_init(st);
-  S.run(pair, wb, we, qB, P, st, lane);
-  finish_block(P, st, pair, split, lane, wave);
+  char* slot = reinterpret_cast<char*>(smem) + (size_t)wave * kQSlotBytes;
+  S.run(pair, wb, we, qB, P, st, slot, lane);
+  finish_block<NW>(P, st, smem + stage_lds_bytes(NW, Src::kQuant) / sizeof(float), pair, split,
+                   lane, wave);
 }
 
-// Log-sum-exp merge of the split partials; one workgroup per KV head.
+// Log-sum-exp merge of the split partials: one thread per output element.
 __global__ __launch_bounds__(256) void merge_kernel(AttnCommon P) {
-  const int64_t pair = blockIdx.x;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= P.pairs * P.G * kHeadDim) return;
+  const int d = (int)(e % kHeadDim);
+  const int hn = (int)((e / kHeadDim) % P.G);
+  const int64_t pair = e / ((int64_t)kHeadDim * P.G);
   const int64_t b = pair / P.KVH;
   const int kvh = (int)(pair % P.KVH);
   const size_t total = (size_t)P.pairs * P.n_splits * P.G;
   const float* wo = P.ws;
   const float* wm = P.ws + total * kHeadDim;
   const float* wl = wm + total;
-  for (int e = threadIdx.x; e < P.G * kHeadDim; e += 256) {
-    const int hn = e / kHeadDim, d = e % kHeadDim;
-    const size_t base = (size_t)pair * P.n_splits * P.G + hn;
-    float M = -INFINITY;
-    for (int s = 0; s < P.n_splits; ++s) M = fmaxf(M, wm[base + (size_t)s * P.G]);
-    const float Mu = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f, acc = 0.f;
-    for (int s = 0; s < P.n_splits; ++s) {
-      const size_t idx = base + (size_t)s * P.G;
-      const float f = __builtin_amdgcn_exp2f(wm[idx] - Mu);
-      L += wl[idx] * f;
-      acc += wo[idx * kHeadDim + d] * f;
-    }
-    P.o[((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + d] = (_Float16)(acc / L);
+  const size_t base = (size_t)pair * P.n_splits * P.G + hn;
+  float M = kMaxSentinel;
+  for (int s = 0; s < P.n_splits; ++s) M = fmaxf(M, wm[base + (size_t)s * P.G]);
+  float L = 0.f, acc = 0.f;
+#pragma unroll 4
+  for (int s = 0; s < P.n_splits; ++s) {
+    const size_t idx = base + (size_t)s * P.G;
+    const float f = __builtin_amdgcn_exp2f(wm[idx] - M);
+    L += wl[idx] * f;
+    acc += wo[idx * kHeadDim + d] * f;
   }
+  P.o[((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + d] = (_Float16)(acc / L);
 }
 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
-// Split-K plan: aim for >= kTargetBlocks workgroups over the whole grid while
-// giving every wave at least kMinTilesPerWave tiles.
-constexpr int64_t kTargetBlocks = 2048;
-constexpr int64_t kMinTilesPerWave = 4;
+// Launch plan.  Aim for kTargetWaves resident waves over the whole chip (256
+// CUs x 2 waves per SIMD x 4 SIMDs), at least kMinTilesPerWave tiles each; a
+// KV head gets up to 8 waves in one workgroup and more waves only through
+// splits (which need the merge pass).
+constexpr int64_t kTargetWaves = 2048;
+constexpr int64_t kMinTilesPerWave = 2;
 
-void plan_splits(int64_t pairs, int64_t n_tiles, int* splits, int* tps) {
-  int64_t max_splits = n_tiles / (kWaves * kMinTilesPerWave);
-  if (max_splits < 1) max_splits = 1;
-  int64_t want = (kTargetBlocks + pairs - 1) / pairs;
-  int64_t s = want < max_splits ? want : max_splits;
-  if (s < 1) s = 1;
+struct Plan {
+  int nw, splits, tps;
+};
+
+Plan make_plan(int64_t pairs, int64_t n_tiles, int G, bool quant) {
+  int64_t wpp = (kTargetWaves + pairs - 1) / pairs;
+  const int64_t cap = (n_tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
+  if (wpp > cap) wpp = cap;
+  if (wpp < 1) wpp = 1;
+  const bool fits8 = merge_lds_bytes(8, G) + stage_lds_bytes(8, quant) <= 65536;
+  Plan p;
+  p.nw = (wpp > 4 && fits8) ? 8 : 4;
+  int64_t s = (wpp + p.nw - 1) / p.nw;
   int64_t t = (n_tiles + s - 1) / s;
   s = (n_tiles + t - 1) / t;
-  *splits = (int)s;
-  *tps = (int)t;
+  p.splits = (int)s;
+  p.tps = (int)t;
+  return p;
 }
 
 int64_t tiles_for(int kind, int64_t n_slots) {
@@ -276,21 +318,48 @@ int launch_status() {
 
 template <class Src>
 int launch_attn(AttnCommon P, const Src& S, size_t ws_bytes, hipStream_t stream) {
-  int splits = 0, tps = 0;
-  plan_splits(P.pairs, P.n_tiles, &splits, &tps);
-  P.n_splits = splits;
-  P.tiles_per_split = tps;
-  if (splits > 1) {
+  const Plan plan = make_plan(P.pairs, P.n_tiles, P.G, Src::kQuant);
+  P.n_splits = plan.splits;
+  P.tiles_per_split = plan.tps;
+  if (plan.splits > 1) {
     if (P.ws == nullptr) return KVDEC_E_WORKSPACE;
-    if (ws_bytes < ws_bytes_for(P.pairs, splits, P.G)) return KVDEC_E_WORKSPACE;
+    if (ws_bytes < ws_bytes_for(P.pairs, plan.splits, P.G)) return KVDEC_E_WORKSPACE;
   }
-  const int64_t blocks = P.pairs * splits;
+  const int64_t blocks = P.pairs * plan.splits;
   if (blocks > 0x7fffffffLL) return KVDEC_E_SHAPE;
-  hipLaunchKernelGGL(attn_kernel<Src>, dim3((unsigned)blocks), dim3(kBlock), 0, stream, P, S);
+  const size_t lds = stage_lds_bytes(plan.nw, Src::kQuant) + merge_lds_bytes(plan.nw, P.G);
+  if (plan.nw == 8)
+    hipLaunchKernelGGL((attn_kernel<Src, 8>), dim3((unsigned)blocks), dim3(64 * 8), lds, stream,
+                       P, S);
+  else
+    hipLaunchKernelGGL((attn_kernel<Src, 4>), dim3((unsigned)blocks), dim3(64 * 4), lds, stream,
+                       P, S);
   int rc = launch_status();
-  if (rc != KVDEC_OK || splits == 1) return rc;
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)P.pairs), dim3(256), 0, stream, P);
+  if (rc != KVDEC_OK || plan.splits == 1) return rc;
+  const int64_t outs = P.pairs * P.G * kHeadDim;
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, stream, P);
   return launch_status();
+}
+
+// Validity ranges of the [sink + window] cache at this length (the
+// _kv_indices rule for the linear layout), clamped into [0, sink + window].
+SlotRanges sparse_ranges(int64_t seq_len, int32_t window, int32_t sink, int32_t layout) {
+  const int64_t S = sink, W = window, n = S + W;
+  auto clamp = [n](int64_t v) { return (int)(v < 0 ? 0 : (v > n ? n : v)); };
+  SlotRanges R;
+  R.va = clamp(seq_len < S ? seq_len : S);
+  if (layout == KVDEC_LAYOUT_LINEAR) {
+    const int64_t lo = 2 * S + W - seq_len;
+    R.vb = clamp(lo > S ? lo : S);
+    R.vc = clamp(n);
+  } else {
+    int64_t nwin = seq_len - S;
+    if (nwin < 0) nwin = 0;
+    if (nwin > W) nwin = W;
+    R.vb = clamp(S);
+    R.vc = clamp(S + nwin);
+  }
+  return R;
 }
 
 }  // namespace
@@ -316,20 +385,20 @@ const char* kvdec_strerror(int code) {
   return "unknown kvdec error";
 }
 
-const char* kvdec_version(void) { return "kvdec 0.1 gfx950"; }
+const char* kvdec_version(void) { return "kvdec 0.2 gfx950"; }
 
 int kvdec_num_splits(int kind, int64_t B, int32_t KVH, int64_t n_slots) {
   if (B < 1 || KVH < 1 || n_slots < 1) return 1;
-  int splits = 1, tps = 1;
-  plan_splits(B * KVH, tiles_for(kind, n_slots), &splits, &tps);
-  return splits;
+  // The plan's split count does not depend on the group size, only the
+  // waves-per-workgroup choice does.
+  return make_plan(B * KVH, tiles_for(kind, n_slots), 8, kind == KVDEC_KIND_KIVI).splits;
 }
 
 size_t kvdec_workspace_bytes(int kind, int64_t B, int32_t H, int32_t KVH, int64_t n_slots,
                              int32_t D) {
   if (check_heads(B, H, KVH, D) != KVDEC_OK || n_slots < 1) return 0;
-  const int splits = kvdec_num_splits(kind, B, KVH, n_slots);
-  return ws_bytes_for(B * KVH, splits, H / KVH);
+  const Plan p = make_plan(B * KVH, tiles_for(kind, n_slots), H / KVH, kind == KVDEC_KIND_KIVI);
+  return ws_bytes_for(B * KVH, p.splits, H / KVH);
 }
 
 int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int dtype, int64_t B,
@@ -351,30 +420,10 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int
   P.G = H / KVH;
   P.n_tiles = (int)tiles_for(KVDEC_KIND_DENSE, L);
   P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
-  P.R = SlotRanges{L, 0, 0};
+  P.R = SlotRanges{(int)L, 0, 0};
   F16Src S{static_cast<const _Float16*>(k), static_cast<const _Float16*>(v), (int)L};
   return launch_attn(P, S, ws_bytes, static_cast<hipStream_t>(stream));
 }
-
-namespace {
-SlotRanges sparse_ranges(int64_t seq_len, int32_t window, int32_t sink, int32_t layout) {
-  const int64_t S = sink, W = window;
-  SlotRanges R;
-  R.va = seq_len < S ? seq_len : S;
-  if (layout == KVDEC_LAYOUT_LINEAR) {
-    const int64_t lo = 2 * S + W - seq_len;
-    R.vb = lo > S ? lo : S;
-    R.vc = S + W;
-  } else {
-    int64_t nwin = seq_len - S;
-    if (nwin < 0) nwin = 0;
-    if (nwin > W) nwin = W;
-    R.vb = S;
-    R.vc = S + nwin;
-  }
-  return R;
-}
-}  // namespace
 
 int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache, void* o,
                         int dtype, int64_t B, int32_t H, int32_t KVH, int64_t seq_len,

@@ -26,11 +26,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kHeadDim = 128;   // D: fixed by the MFMA tiling below
-constexpr int kTile = 32;       // tokens per tile
-constexpr int kWaves = 4;       // waves per workgroup
-constexpr int kBlock = 64 * kWaves;
+constexpr int kTile = 32;       // tokens per tile (one KIVI group)
 constexpr int kMaxGroup = 16;   // query heads per KV head (MFMA columns)
-constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ half8 as_h8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 __device__ __forceinline__ u32x4 as_u4(half8 v) { return __builtin_bit_cast(u32x4, v); }
@@ -43,18 +40,11 @@ __device__ __forceinline__ float4v mfma16x16x32(u32x4 a, half8 b, float4v c) {
 // of two stacked 16x16 QK blocks, reused as the PV reduction order.
 __device__ __forceinline__ int tau(int g, int j) { return 16 * (j >> 2) + 4 * g + (j & 3); }
 
-// One 32-token tile in MFMA operand layout (fp16):
-//   k[blk][c] : K[token 16*blk + t][channels 32c + 8g .. +7]
-//   v[j]      : V[token tau(g, j)][channels 8m .. 8m+7]
-struct Tile {
-  u32x4 k[2][4];
-  u32x4 v[8];
-};
-
 // Per-wave online-softmax state.  Lane (n, g) owns head n; logits are kept
 // in the log2 domain (scaled by sm_scale * log2(e)).
 //   O[jj][r] : unnormalised output of head n, channel 8*(4g + r) + jj
-//   m        : running max, identical in the four lanes of a head
+//   m        : reference max of head n, identical in the four lanes of a head;
+//              starts at a finite sentinel so exp2(-inf - m) is 0, never NaN
 //   l        : this lane's share of the softmax denominator
 struct WaveState {
   float4v O[8];
@@ -62,120 +52,177 @@ struct WaveState {
   float l;
 };
 
+constexpr float kMaxSentinel = -1e30f;
+// The reference max is refreshed only when a tile's max exceeds it by more
+// than this (log2 units), so probabilities stay <= 2^8: exact range for the
+// fp16 P operand, and most tiles skip the cross-lane max and the O rescale.
+constexpr float kRescaleSlack = 8.0f;
+
 __device__ __forceinline__ void wave_state_init(WaveState& st) {
 #pragma unroll
   for (int jj = 0; jj < 8; ++jj) st.O[jj] = float4v{0.f, 0.f, 0.f, 0.f};
-  st.m = -INFINITY;
+  st.m = kMaxSentinel;
   st.l = 0.f;
 }
 
-// Slot validity: s < va, or vb <= s < vc.  Dense uses va = L; the sparse and
-// KIVI caches use the StreamingLLM sink / window ranges.
+// Slot validity inside one KV head: s < va, or vb <= s < vc (slot numbers of
+// one head fit in 31 bits).  Dense uses va = L; the sparse and KIVI caches
+// use the StreamingLLM sink / window ranges.
 struct SlotRanges {
-  int64_t va, vb, vc;
+  int va, vb, vc;
 };
 
-__device__ __forceinline__ bool slot_valid(const SlotRanges& R, int64_t s) {
+__device__ __forceinline__ bool slot_valid(const SlotRanges& R, int s) {
   return s < R.va || (s >= R.vb && s < R.vc);
 }
 
-// Consume one tile: QK on MFMA, masking, online softmax, PV on MFMA.
-// `slot0` is the cache slot of the tile's token 0, `xlim` the number of
-// tokens of the tile that belong to the region (the rest are masked).
-__device__ __forceinline__ void tile_step(Tile& T, const half8 (&qB)[4], int64_t slot0,
-                                          int xlim, const SlotRanges& R, float scale_log2,
-                                          WaveState& st, int lane) {
+// True when every token of the 32-token tile starting at slot0 is valid
+// (wave-uniform: slot0 and the ranges are the same in every lane).
+__device__ __forceinline__ bool tile_fully_valid(const SlotRanges& R, int slot0) {
+  const int last = slot0 + kTile - 1;
+  return last < R.va || (slot0 >= R.vb && last < R.vc);
+}
+
+// Validity bits of the lane's 8 tokens tau(g, j) of the tile at slot0
+// (tokens at or past xlim do not belong to the region).
+__device__ __forceinline__ uint32_t tile_valid_bits(const SlotRanges& R, int slot0, int xlim,
+                                                    int lane) {
   const int g = lane >> 4;
-
-  float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    s0 = mfma16x16x32(T.k[0][c], qB[c], s0);
-    s1 = mfma16x16x32(T.k[1][c], qB[c], s1);
-  }
-
-  float x[8];
-  bool all_ok = true;
+  uint32_t bits = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int tok = tau(g, j);
-    const float raw = (j < 4 ? s0[j & 3] : s1[j & 3]) * scale_log2;
-    const bool ok = tok < xlim && slot_valid(R, slot0 + tok);
-    all_ok = all_ok && ok;
-    x[j] = ok ? raw : -INFINITY;
-    if (!ok) T.v[j] = u32x4{0u, 0u, 0u, 0u};   // masked rows contribute exact zeros
+    bits |= (tok < xlim && slot_valid(R, slot0 + tok)) ? (1u << j) : 0u;
   }
-  (void)all_ok;
+  return bits;
+}
 
-  float mt = x[0];
+// Consume one tile: QK on MFMA, masking, online softmax, PV on MFMA.
+//   kop(blk, c) -> u32x4 : K operand of block blk, channel chunk c
+//                          (K[token 16*blk + t][channels 32c + 8g .. +7])
+//   vop(w, j)   -> u32   : dword w of V row j, i.e. channels 8m+2w, 8m+2w+1
+//                          of token tau(g, j)
+// FULL: every token of the tile is valid.  Otherwise bit j of `valid` says
+// whether the lane's token tau(g, j) is, and masked logits become -inf.
+template <bool FULL, class KOp, class VOp>
+__device__ __forceinline__ void tile_body(KOp&& kop, VOp&& vop, uint32_t valid,
+                                          const half8 (&qB)[4], float scale_log2, WaveState& st) {
+  float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 1; j < 8; ++j) mt = fmaxf(mt, x[j]);
-  mt = fmaxf(mt, __shfl_xor(mt, 16));
-  mt = fmaxf(mt, __shfl_xor(mt, 32));
-  const float mnew = fmaxf(st.m, mt);
-  const float mu = (mnew == -INFINITY) ? 0.f : mnew;
-  const float alpha = __builtin_amdgcn_exp2f(st.m - mu);
+  for (int c = 0; c < 4; ++c) {
+    s0 = mfma16x16x32(kop(0, c), qB[c], s0);
+    s1 = mfma16x16x32(kop(1, c), qB[c], s1);
+  }
+
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    x[j] = (j < 4 ? s0[j & 3] : s1[j & 3]) * scale_log2;
+    if (!FULL) x[j] = ((valid >> j) & 1u) ? x[j] : -INFINITY;
+  }
+  float lmax = x[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) lmax = fmaxf(lmax, x[j]);
+
+  // Refresh the reference max only if some lane's tile max exceeds it by
+  // more than kRescaleSlack (wave-uniform branch).
+  if (__ballot(lmax > st.m + kRescaleSlack)) {
+    float mt = fmaxf(lmax, __shfl_xor(lmax, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mnew = fmaxf(st.m, mt);
+    const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
+    st.l *= alpha;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) st.O[jj] = st.O[jj] * alpha;
+    st.m = mnew;
+  }
 
   half8 pB;
   float ls = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float p = __builtin_amdgcn_exp2f(x[j] - mu);
+    const float p = __builtin_amdgcn_exp2f(x[j] - st.m);
     ls += p;
     pB[j] = (_Float16)p;
   }
-  st.l = st.l * alpha + ls;
-  st.m = mnew;
+  st.l += ls;
 
 #pragma unroll
-  for (int jj = 0; jj < 8; ++jj) {
-    const int w = jj >> 1;
-    const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-    u32x4 a;
-    a[0] = __builtin_amdgcn_perm(T.v[1][w], T.v[0][w], sel);
-    a[1] = __builtin_amdgcn_perm(T.v[3][w], T.v[2][w], sel);
-    a[2] = __builtin_amdgcn_perm(T.v[5][w], T.v[4][w], sel);
-    a[3] = __builtin_amdgcn_perm(T.v[7][w], T.v[6][w], sel);
-    st.O[jj] = st.O[jj] * alpha;
-    st.O[jj] = mfma16x16x32(a, pB, st.O[jj]);
+  for (int w = 0; w < 4; ++w) {
+    uint32_t d[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) d[j] = vop(w, j);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t sel = e ? 0x07060302u : 0x05040100u;
+      u32x4 a;
+      a[0] = __builtin_amdgcn_perm(d[1], d[0], sel);
+      a[1] = __builtin_amdgcn_perm(d[3], d[2], sel);
+      a[2] = __builtin_amdgcn_perm(d[5], d[4], sel);
+      a[3] = __builtin_amdgcn_perm(d[7], d[6], sel);
+      st.O[2 * w + e] = mfma16x16x32(a, pB, st.O[2 * w + e]);
+    }
   }
 }
 
-// Load an fp16 tile from a [rows, 128] region (rows of this KV head).  Rows
-// past the end are clamped to the last row; tile_step masks them.
+// ---------------------------------------------------------------------------
+// fp16 tiles
+// ---------------------------------------------------------------------------
+
+// One 32-token fp16 tile in MFMA operand layout:
+//   k[blk][c] : K[token 16*blk + t][channels 32c + 8g .. +7]
+//   v[j]      : V[token tau(g, j)][channels 8m .. 8m+7]
+struct Tile {
+  u32x4 k[2][4];
+  u32x4 v[8];
+};
+
+// Consume an fp16 tile.  V rows of masked tokens are replaced by zeros at use
+// time: unwritten cache slots may hold anything, including non-finite values.
+__device__ __forceinline__ void tile_step(const Tile& T, const half8 (&qB)[4], int slot0,
+                                          const SlotRanges& R, float scale_log2, WaveState& st,
+                                          int lane) {
+  auto kop = [&](int blk, int c) { return T.k[blk][c]; };
+  if (tile_fully_valid(R, slot0)) {
+    tile_body<true>(kop, [&](int w, int j) { return T.v[j][w]; }, 0u, qB, scale_log2, st);
+  } else {
+    const uint32_t valid = tile_valid_bits(R, slot0, kTile, lane);
+    tile_body<false>(kop, [&](int w, int j) { return ((valid >> j) & 1u) ? T.v[j][w] : 0u; },
+                     valid, qB, scale_log2, st);
+  }
+}
+
+// Load an fp16 tile from a [rows, 128] region (one KV head, base pointers
+// uniform across the wave).  Rows past the end are clamped to the last row;
+// their slots are invalid, so tile_step masks them.
 __device__ __forceinline__ void load_f16_tile(const _Float16* __restrict__ kb,
                                               const _Float16* __restrict__ vb, int row0,
                                               int rows, int lane, Tile& T) {
   const int t = lane & 15, g = lane >> 4;
+  const char* kc = reinterpret_cast<const char*>(kb);
+  const char* vc = reinterpret_cast<const char*>(vb);
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
-    int r = row0 + 16 * blk + t;
-    r = r < rows ? r : rows - 1;
-    const u32x4* p = reinterpret_cast<const u32x4*>(kb + (size_t)r * kHeadDim) + g;
+    const int r = min(row0 + 16 * blk + t, rows - 1);
+    const uint32_t off = (uint32_t)r * (kHeadDim * 2) + 16u * g;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) T.k[blk][c] = p[4 * c];
+    for (int c = 0; c < 4; ++c) T.k[blk][c] = *reinterpret_cast<const u32x4*>(kc + off + 64u * c);
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    int r = row0 + tau(g, j);
-    r = r < rows ? r : rows - 1;
-    T.v[j] = *(reinterpret_cast<const u32x4*>(vb + (size_t)r * kHeadDim) + t);
+    const int r = min(row0 + tau(g, j), rows - 1);
+    T.v[j] = *reinterpret_cast<const u32x4*>(vc + (uint32_t)r * (kHeadDim * 2) + 16u * t);
   }
 }
 
-// Raw (still packed) KIVI tile: 32 tokens of one quantized region, i.e.
-// exactly one quantization group of K.
-//   kc[blk][c] : K code bytes of token row (16*blk + t)/4, channels 32c+8g..+7
-//   ks/kz[c]   : K scale / zero of channels 32c+8g..+7 (fp16 x 8)
-//   vc[j]      : V code bytes (2) of token tau(g, j), channels 8m..8m+7
-//   vs/vz[j]   : V scale / zero of that token, channel group m/4 (fp16)
-struct RawQTile {
-  u32x2 kc[2][4];
-  u32x4 ks[4], kz[4];
-  uint32_t vc[8], vs[8], vz[8];
-};
+// ---------------------------------------------------------------------------
+// KIVI 2-bit tiles
+// ---------------------------------------------------------------------------
 
-// Device pointers of one KIVI-quantized region, bound to one KV head.
+// Device pointers of one KIVI-quantized region, bound to one KV head.  A
+// 32-token tile tq is one quantization group: 1 KB of K codes (8 byte rows of
+// 128 channels), 128 K scales and zeros, 1 KB of V codes (32 tokens x 32
+// bytes), 32 x 4 V scales and zeros -- six contiguous pieces.
 struct QRegion {
   const uint8_t* kp;     // [ntok/4][128]
   const _Float16* ks;    // [ntok/32][128]
@@ -185,67 +232,119 @@ struct QRegion {
   const _Float16* vz;
 };
 
-__device__ __forceinline__ void load_q_tile(const QRegion& Q, int tq, int lane, RawQTile& X) {
-  const int t = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk) {
-    const int brow = 8 * tq + 4 * blk + (t >> 2);
-    const uint8_t* p = Q.kp + (size_t)brow * kHeadDim + 8 * g;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) X.kc[blk][c] = *reinterpret_cast<const u32x2*>(p + 32 * c);
-  }
-  const _Float16* sp = Q.ks + (size_t)tq * kHeadDim + 8 * g;
-  const _Float16* zp = Q.kz + (size_t)tq * kHeadDim + 8 * g;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    X.ks[c] = *reinterpret_cast<const u32x4*>(sp + 32 * c);
-    X.kz[c] = *reinterpret_cast<const u32x4*>(zp + 32 * c);
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int tok = 32 * tq + tau(g, j);
-    X.vc[j] = *reinterpret_cast<const uint16_t*>(Q.vp + (size_t)tok * 32 + 2 * t);
-    X.vs[j] = *reinterpret_cast<const uint16_t*>(Q.vs + (size_t)tok * 4 + (t >> 2));
-    X.vz[j] = *reinterpret_cast<const uint16_t*>(Q.vz + (size_t)tok * 4 + (t >> 2));
-  }
+// A tile as loaded from HBM: every lane fetches a 1/64 slice of each piece
+// with one coalesced load (12 VGPRs per tile, no duplication across lanes).
+struct QTileRaw {
+  u32x4 kc;            // K code bytes [16L, 16L+16)
+  u32x4 vc;            // V code bytes [16L, 16L+16)
+  uint32_t ks, kz;     // K scale / zero of channels 2L, 2L+1
+  uint32_t vs, vz;     // V scale / zero of token L/2, groups 2(L%2), 2(L%2)+1
+};
+
+__device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, int lane, QTileRaw& X) {
+  X.kc = *reinterpret_cast<const u32x4*>(Q.kp + (size_t)tq * 1024 + 16 * lane);
+  X.vc = *reinterpret_cast<const u32x4*>(Q.vp + (size_t)tq * 1024 + 16 * lane);
+  X.ks = *reinterpret_cast<const uint32_t*>(Q.ks + (size_t)tq * kHeadDim + 2 * lane);
+  X.kz = *reinterpret_cast<const uint32_t*>(Q.kz + (size_t)tq * kHeadDim + 2 * lane);
+  X.vs = *reinterpret_cast<const uint32_t*>(Q.vs + (size_t)tq * 128 + 2 * lane);
+  X.vz = *reinterpret_cast<const uint32_t*>(Q.vz + (size_t)tq * 128 + 2 * lane);
 }
 
-// fp16 bit patterns 0x6400 | c encode 1024 + c exactly for c in 0..3, so
-// (0x6400|c) - (1024 + z) == c - z exactly for integer |c - z| <= 2048; the
-// product with the fp16 scale is then the only rounding (to fp16).
-__device__ __forceinline__ void decode_q_tile(const RawQTile& X, int lane, Tile& T) {
-  const int t = lane & 15;
-  const uint32_t sh = 2u * (uint32_t)(t & 3);
-  const _Float16 k1024 = (_Float16)1024.0f;
+// Per-wave LDS staging slot of one tile (bytes): K codes [0,1024), K scales
+// [1024,1280), K zeros [1280,1536), V codes [1536,2560), V (scale, zero)
+// pairs [2560,3072) at 2560 + 16*token + 4*group.
+constexpr int kQSlotBytes = 3072;
+
+__device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
+  *reinterpret_cast<u32x4*>(slot + 16 * lane) = X.kc;
+  *reinterpret_cast<uint32_t*>(slot + 1024 + 4 * lane) = X.ks;
+  *reinterpret_cast<uint32_t*>(slot + 1280 + 4 * lane) = X.kz;
+  *reinterpret_cast<u32x4*>(slot + 1536 + 16 * lane) = X.vc;
+  u32x2 sz;
+  sz[0] = __builtin_amdgcn_perm(X.vz, X.vs, 0x05040100u);   // (scale, zero) of group 2(L%2)
+  sz[1] = __builtin_amdgcn_perm(X.vz, X.vs, 0x07060302u);   // (scale, zero) of group 2(L%2)+1
+  *reinterpret_cast<u32x2*>(slot + 2560 + 8 * lane) = sz;
+}
+
+// The V part of a staged tile in MFMA operand layout (read back from the LDS
+// slot; the K operands are read from the slot on demand):
+//   vc[i]  : V code bytes (2 x 8 bit) of tokens tau(g, 2i) (low 16 bits) and
+//            tau(g, 2i+1) (high 16 bits), channels 8m..8m+7
+//   vsz[j] : V scale (low half) and zero (high half) of token tau(g, j),
+//            channel group m/4
+struct QTileV {
+  uint32_t vc[4];
+  uint32_t vsz[8];
+};
+
+__device__ __forceinline__ void read_q_v(const char* slot, int lane, QTileV& X) {
+  const int t = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const half8 s8 = as_h8(X.ks[c]);
-    const half8 zz = as_h8(X.kz[c]) + k1024;
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const uint32_t c0 = (X.kc[blk][c][0] >> sh) & 0x03030303u;
-      const uint32_t c1 = (X.kc[blk][c][1] >> sh) & 0x03030303u;
-      u32x4 mg;
-      mg[0] = __builtin_amdgcn_perm(c0, 0x64646464u, 0x00050004u);
-      mg[1] = __builtin_amdgcn_perm(c0, 0x64646464u, 0x00070006u);
-      mg[2] = __builtin_amdgcn_perm(c1, 0x64646464u, 0x00050004u);
-      mg[3] = __builtin_amdgcn_perm(c1, 0x64646464u, 0x00070006u);
-      T.k[blk][c] = as_u4((as_h8(mg) - zz) * s8);
-    }
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = *reinterpret_cast<const uint16_t*>(slot + 1536 + tau(g, 2 * i) * 32 + 2 * t);
+    const uint32_t hi =
+        *reinterpret_cast<const uint16_t*>(slot + 1536 + tau(g, 2 * i + 1) * 32 + 2 * t);
+    X.vc[i] = lo | (hi << 16);
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t b = X.vc[j];
-    const uint32_t t0 = b | (b << 14);
-    u32x4 mg;
-    mg[0] = (t0 & 0x00030003u) | 0x64006400u;
-    mg[1] = ((t0 >> 4) & 0x00030003u) | 0x64006400u;
-    mg[2] = ((t0 >> 8) & 0x00030003u) | 0x64006400u;
-    mg[3] = ((t0 >> 12) & 0x00030003u) | 0x64006400u;
-    const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)X.vs[j]);
-    const _Float16 zz = __builtin_bit_cast(_Float16, (uint16_t)X.vz[j]) + k1024;
-    T.v[j] = as_u4((as_h8(mg) - zz) * s);
-  }
+  for (int j = 0; j < 8; ++j)
+    X.vsz[j] = *reinterpret_cast<const uint32_t*>(slot + 2560 + tau(g, j) * 16 + 4 * (t >> 2));
+}
+
+// fp16 bit patterns 0x6400 | c encode 1024 + c exactly for c in 0..3; one
+// packed subtract of 1024 gives the code itself, a second subtract of the
+// stored fp16 zero gives c - z exactly while |c - z| <= 2048 (a rounding of
+// at most 2^-11 relative beyond), and the multiply by the fp16 scale is the
+// one rounding of the dequantized value (to fp16, the MFMA input type).
+
+// K operand of block blk, chunk c, read from the staged slot: the code bytes
+// of byte row (16*blk + t)/4 and the scales / zeros of channels 32c+8g..+7.
+__device__ __forceinline__ u32x4 decode_q_k(const char* slot, int blk, int c, int lane) {
+  const int t = lane & 15, g = lane >> 4;
+  const uint32_t sh = 2u * (uint32_t)(t & 3);   // token 16*blk + t sits at bits 2*(t%4)
+  const u32x2 kc =
+      *reinterpret_cast<const u32x2*>(slot + (4 * blk + (t >> 2)) * 128 + 32 * c + 8 * g);
+  const u32x4 ks = *reinterpret_cast<const u32x4*>(slot + 1024 + 2 * (32 * c + 8 * g));
+  const u32x4 kz = *reinterpret_cast<const u32x4*>(slot + 1280 + 2 * (32 * c + 8 * g));
+  const uint32_t c0 = (kc[0] >> sh) & 0x03030303u;
+  const uint32_t c1 = (kc[1] >> sh) & 0x03030303u;
+  u32x4 mg;
+  mg[0] = __builtin_amdgcn_perm(c0, 0x64646464u, 0x00050004u);
+  mg[1] = __builtin_amdgcn_perm(c0, 0x64646464u, 0x00070006u);
+  mg[2] = __builtin_amdgcn_perm(c1, 0x64646464u, 0x00050004u);
+  mg[3] = __builtin_amdgcn_perm(c1, 0x64646464u, 0x00070006u);
+  const half8 code = as_h8(mg) - (_Float16)1024.0f;
+  return as_u4((code - as_h8(kz)) * as_h8(ks));
+}
+
+// Dword w of V row j: channels 8m+2w and 8m+2w+1 sit at bits 4w and 4w+2 of
+// the row's 16 code bits; b | (b << 14) moves the second one to bit 16 + 4w.
+__device__ __forceinline__ uint32_t decode_q_v(const QTileV& X, int w, int j) {
+  const uint32_t b = (X.vc[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+  const uint32_t t0 = b | (b << 14);
+  const uint32_t mg = ((t0 >> (4 * w)) & 0x00030003u) | 0x64006400u;
+  // broadcast scale (low half) and zero (high half) to both halves
+  const half2v s2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(X.vsz[j], X.vsz[j], 0x01000100u));
+  const half2v z2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(X.vsz[j], X.vsz[j], 0x03020302u));
+  const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+  const half2v code = __builtin_bit_cast(half2v, mg) - k1024;
+  return __builtin_bit_cast(uint32_t, (code - z2) * s2);
+}
+
+// Consume one KIVI tile staged in the wave's LDS slot.  Masked tokens get
+// probability exactly 0 and their dequantized values are finite, so no row is
+// zeroed (the reference masks only its fp16 residual loads).
+__device__ __forceinline__ void q_tile_step(const char* slot, const half8 (&qB)[4], int slot0,
+                                            int xlim, const SlotRanges& R, float scale_log2,
+                                            WaveState& st, int lane) {
+  QTileV X;
+  read_q_v(slot, lane, X);
+  auto kop = [&](int blk, int c) { return decode_q_k(slot, blk, c, lane); };
+  auto vop = [&](int w, int j) { return decode_q_v(X, w, j); };
+  if (xlim == kTile && tile_fully_valid(R, slot0))
+    tile_body<true>(kop, vop, 0u, qB, scale_log2, st);
+  else
+    tile_body<false>(kop, vop, tile_valid_bits(R, slot0, xlim, lane), qB, scale_log2, st);
 }
 
 }  // namespace kvdec

@@ -56,19 +56,22 @@ def test_strerror_and_version():
 
 
 def test_split_plan_and_workspace_arithmetic():
-    # the metric configuration: dense over 163840 tokens splits, sparse/KIVI W=256 do not
-    s_dense = K.lib.kvdec_num_splits(K.KIND_DENSE, 32, 8, 163840)
-    assert s_dense > 1
-    assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 32, 64, 8, 163840, 128) == 256 * s_dense * 8 * 130 * 4
-    assert K.lib.kvdec_num_splits(K.KIND_SPARSE, 32, 8, 260) == 1
-    assert K.lib.kvdec_workspace_bytes(K.KIND_SPARSE, 32, 64, 8, 260, 128) == 0
-    assert K.lib.kvdec_num_splits(K.KIND_KIVI, 32, 8, 256) == 1
-    assert K.lib.kvdec_workspace_bytes(K.KIND_KIVI, 32, 64, 8, 256, 128) == 0
-    # every split keeps at least 4 tiles per wave
-    for L in (1, 2, 100, 8192, 32768, 131072, 163840):
-        s = K.lib.kvdec_num_splits(K.KIND_DENSE, 32, 8, L)
-        tiles = -(-L // 32)
-        assert s == 1 or tiles / s >= 16
+    # at the metric shapes (B*KVH = 256 KV heads fill the GPU) every path runs
+    # in one pass: no split, no workspace
+    for kind, n in ((K.KIND_DENSE, 163840), (K.KIND_DENSE, 32768), (K.KIND_SPARSE, 260),
+                    (K.KIND_SPARSE, 16388), (K.KIND_KIVI, 256), (K.KIND_KIVI, 4096)):
+        assert K.lib.kvdec_num_splits(kind, 32, 8, n) == 1, (kind, n)
+        assert K.lib.kvdec_workspace_bytes(kind, 32, 64, 8, n, 128) == 0, (kind, n)
+    # a small batch splits the context and needs G x (128 + 2) floats per split
+    s = K.lib.kvdec_num_splits(K.KIND_DENSE, 1, 8, 163840)
+    assert s > 1
+    assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 1, 64, 8, 163840, 128) == 8 * s * 8 * 130 * 4
+    # every split keeps at least 2 tiles per wave of an 8-wave workgroup
+    for B in (1, 2, 4, 32):
+        for L in (1, 2, 100, 8192, 32768, 131072, 163840):
+            s = K.lib.kvdec_num_splits(K.KIND_DENSE, B, 8, L)
+            tiles = -(-L // 32)
+            assert s == 1 or tiles / s >= 16, (B, L, s)
     # invalid heads -> no workspace
     assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 32, 64, 7, 1000, 128) == 0
     assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 32, 64, 8, 1000, 64) == 0
