@@ -13,7 +13,9 @@ from conftest import ROOT
 import _kvdec as K
 
 HEADER = os.path.join(ROOT, "include", "kvdec.h")
-FAKE = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+# Never dereferenced: every call below is built to fail host-side validation
+# before any launch (a launch on these pointers would fault the GPU).
+FAKE = ctypes.c_void_p(0x1000)
 
 E = {
     "NULL": -1, "SHAPE": -2, "DTYPE": -3, "GROUP": -4, "DGROUP": -5, "WORKSPACE": -6,
@@ -96,8 +98,10 @@ def test_dense_validation():
     assert _dense(B=0) == E["SHAPE"]
     assert _dense(L=0) == E["SEQLEN"]
     assert _dense(L=1 << 23) == E["SHAPE"]        # 32-bit in-head offsets
-    assert _dense(L=163840) == E["WORKSPACE"]     # needs split-K workspace
-    assert _dense(L=163840, ws=FAKE, wsb=16) == E["WORKSPACE"]
+    # B=1: the long context is split, so a workspace is required (these
+    # calls must fail validation: FAKE pointers are never launched on)
+    assert _dense(B=1, L=163840) == E["WORKSPACE"]
+    assert _dense(B=1, L=163840, ws=FAKE, wsb=16) == E["WORKSPACE"]
 
 
 def _sparse(**kw):
@@ -118,7 +122,7 @@ def test_sparse_validation():
     assert _sparse(W=0, S=0) == E["WINDOW"]
     assert _sparse(layout=2) == E["UNSUPPORTED"]
     assert _sparse(layout=1, W=0) == E["WINDOW"]
-    assert _sparse(W=16384) == E["WORKSPACE"]
+    assert _sparse(B=1, W=16384) == E["WORKSPACE"]
 
 
 def _kivi(ptrs=None, **kw):
@@ -145,7 +149,7 @@ def test_kivi_validation():
     assert _kivi(W=128 + 48) == E["GROUP"]                            # window-old not whole groups
     assert _kivi(seq_len=0) == E["SEQLEN"]
     assert _kivi(KVH=3) == E["SHAPE"]
-    assert _kivi(W=8192) == E["WORKSPACE"]
+    assert _kivi(B=1, W=8192) == E["WORKSPACE"]
 
 
 def _quant(fn, **kw):
