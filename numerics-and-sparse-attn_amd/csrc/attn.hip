@@ -2,13 +2,21 @@
 // sink+window decode and the fused KIVI-2bit decode, plus their C-ABI entry
 // points (declared in include/kvdec.h).
 //
-// One workgroup = one (KV head, split) work item of 4 or 8 waves.  Each wave
-// streams a contiguous run of 32-token tiles of that KV head through MFMA
+// One workgroup of 8 waves = one (KV head, split) work unit.  The unit's
+// 32-token tiles form a work queue: wave w takes tiles w and w + 8 at launch
+// (their loads are the first thing the wave issues) and then claims further
+// tiles from a counter in LDS, so waves that the SIMD arbiter serves later
+// simply end up with fewer tiles.  Each wave streams its tiles through MFMA
 // (all GQA query heads of the KV head at once, so each K/V byte is read
 // once), keeps an online softmax, and the waves merge through LDS.  With one
 // split the workgroup writes the fp16 output directly; otherwise it writes an
 // fp32 partial (m, l, acc) and merge_kernel combines the splits.  At the
 // benchmark shapes (B*KVH = 256 KV heads) every path runs in one pass.
+//
+// KIVI units have two queues: the fp16 residual tiles go to the first waves
+// (one each while there are enough waves), the quantized tiles (sink group
+// first, then the window-old groups) to the others; a wave that finishes its
+// residual tiles joins the quantized queue.
 
 #include "kvdec_device.h"
 #include "kvdec.h"
@@ -16,6 +24,16 @@
 using namespace kvdec;
 
 namespace {
+
+constexpr int kWaves = 8;                        // waves per workgroup
+constexpr int kThreads = 64 * kWaves;
+
+#ifndef KVDEC_RES_FIRST
+#define KVDEC_RES_FIRST 1
+#endif
+#ifndef KVDEC_Q_SLEEP
+#define KVDEC_Q_SLEEP 0
+#endif
 
 struct AttnCommon {
   const _Float16* q;     // [B, H, 128]
@@ -28,76 +46,214 @@ struct AttnCommon {
   SlotRanges R;
 };
 
-__device__ __forceinline__ void load_q_operand(const AttnCommon& P, int64_t b, int kvh, int lane,
-                                               half8 (&qB)[4]) {
-  const int n = lane & 15, g = lane >> 4;
-  if (n < P.G) {
-    const u32x4* qp = reinterpret_cast<const u32x4*>(
-                          P.q + ((size_t)b * P.H + (size_t)kvh * P.G + n) * kHeadDim) + g;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) qB[c] = as_h8(qp[4 * c]);
-  } else {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) qB[c] = as_h8(u32x4{0u, 0u, 0u, 0u});
+// LDS of a workgroup (bytes): two work counters, the per-wave max / sum of
+// 16 heads, a 256-byte scratch area per wave, then one 8 KB slot per wave
+// (K tile staging, KIVI tile staging, and at the end that wave's partial
+// output rows).
+constexpr int kLdsCtr = 0;
+constexpr int kLdsM = 16;
+constexpr int kLdsL = kLdsM + kWaves * kMaxGroup * 4;
+constexpr int kLdsTmp = kLdsL + kWaves * kMaxGroup * 4;
+constexpr int kLdsSlots = (kLdsTmp + kWaves * 256 + 255) & ~255;
+constexpr int kLdsBytes = kLdsSlots + kWaves * kSlotBytes;
+static_assert(kMaxGroup * kHeadDim * 4 <= kSlotBytes, "partial output must fit a wave slot");
+
+// Everything a tile step needs besides the tile itself.
+struct StepCtx {
+  half8 qB[4];
+  float scale_log2;
+  SlotRanges R;
+  char* lds;    // workgroup LDS base
+  char* slot;   // this wave's slot
+  int lane;
+};
+
+// Claim the next item of a dynamic queue (wave-uniform result).
+__device__ __forceinline__ int grab(int* ctr, int lane) {
+  int v = 0;
+  if (lane == 0) v = atomicAdd(ctr, 1);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// fp16 tiles [tile0, tile0 + n) of one region of one KV head; region row r
+// is slot slot_base + r.
+struct F16Items {
+  typedef F16Raw Raw;
+  rsrc_t rk, rv;
+  int tile0, n, slot_base;
+  __device__ __forceinline__ void load(int i, Raw& X, int lane) const {
+    load_f16(rk, rv, i < n ? (uint32_t)(tile0 + i) * kSlotBytes : kOOB, lane, X);
+  }
+  typedef WaveState State;
+  __device__ __forceinline__ void step(int i, const Raw& X, State& st, const StepCtx& c) const {
+    f16_tile_step(X, c.slot, c.qB, slot_base + kTile * (tile0 + i), c.R, c.scale_log2, st, c.lane);
+  }
+};
+
+// The accumulators a quantized tile updates.
+struct QRef {
+  WaveState& st;
+  QState& qs;
+};
+
+// Quantized tiles of one KV head: item 0 is the sink group (`sink` real
+// tokens at slots 0..sink-1), item i > 0 is window-old group i-1 (slots
+// sink + 32(i-1) ..).  MIXED: the wave also holds fp16-tile accumulators.
+template <bool MIXED>
+struct QItems {
+  typedef QTileRaw Raw;
+  typedef QRef State;
+  QRegion sinkq, winq;
+  int n, sink;
+  __device__ __forceinline__ void load(int i, Raw& X, int lane) const {
+    const bool s = i == 0;
+    QRegion Q;
+    Q.kp = s ? sinkq.kp : winq.kp;
+    Q.ks = s ? sinkq.ks : winq.ks;
+    Q.kz = s ? sinkq.kz : winq.kz;
+    Q.vp = s ? sinkq.vp : winq.vp;
+    Q.vs = s ? sinkq.vs : winq.vs;
+    Q.vz = s ? sinkq.vz : winq.vz;
+    load_q_raw(Q, s ? 0 : i - 1, i < n, lane, X);
+  }
+  __device__ __forceinline__ void step(int i, const Raw& X, State& s, const StepCtx& c) const {
+    const bool sk = i == 0;
+    q_tile_step<MIXED>(X, c.slot, c.qB, sk ? 0 : sink + kTile * (i - 1), sk ? sink : kTile, c.R,
+                       c.scale_log2, s.st, s.qs, c.lane);
+  }
+};
+
+// Two-deep prefetch ring over one queue.  The loads of both entries are in
+// flight before the first step; every refill is issued unconditionally
+// (items past the queue load nothing), which keeps the memory-counter waits
+// of the steps exact.
+template <class Items>
+struct Ring {
+  typename Items::Raw A, B;
+  int ia, ib;
+};
+
+template <class Items>
+__device__ __forceinline__ void ring_begin(const Items& it, Ring<Items>& r, int s0, int s1,
+                                           int lane) {
+  r.ia = s0;
+  r.ib = s1;
+  it.load(r.ia, r.A, lane);
+  it.load(r.ib, r.B, lane);
+}
+
+// Static queue: the two entries are all the wave gets.
+template <class Items>
+__device__ __forceinline__ void ring_run_static(const Items& it, Ring<Items>& r,
+                                                typename Items::State& st, const StepCtx& c) {
+  if (r.ia < it.n) it.step(r.ia, r.A, st, c);
+  if (r.ib < it.n) it.step(r.ib, r.B, st, c);
+}
+
+// Dynamic queue: refill each entry from the counter as soon as it is used.
+template <class Items>
+__device__ __forceinline__ void ring_run_dynamic(const Items& it, Ring<Items>& r, int* ctr,
+                                                 typename Items::State& st, const StepCtx& c) {
+  for (;;) {
+    if (r.ia >= it.n) break;
+    int nx = grab(ctr, c.lane);
+    it.step(r.ia, r.A, st, c);
+    r.ia = nx;
+    it.load(r.ia, r.A, c.lane);
+    if (r.ib >= it.n) break;
+    nx = grab(ctr, c.lane);
+    it.step(r.ib, r.B, st, c);
+    r.ib = nx;
+    it.load(r.ib, r.B, c.lane);
   }
 }
 
-// LDS of a workgroup: the per-wave KIVI staging slots (quantized sources
-// only), then the merge area -- per wave, the max and sum of 16 heads and the
-// G x 128 partial outputs (rows padded by 4 floats).
-constexpr int kORow = kHeadDim + 4;
-__host__ __device__ constexpr size_t merge_lds_bytes(int nw, int G) {
-  return (size_t)(2 * nw * kMaxGroup + nw * G * kORow) * sizeof(float);
-}
-__host__ __device__ constexpr size_t stage_lds_bytes(int nw, bool quant) {
-  return quant ? (size_t)nw * kQSlotBytes : 0;
+// Publishing a wave's partial result for the workgroup merge: its max and
+// softmax sum per head, and its unnormalised output rows [head][128 fp32] in
+// its own LDS slot (16-byte chunks XOR-swizzled by head), so no wave waits
+// to overwrite another's staging data.
+__device__ __forceinline__ uint32_t row_off(int head, int chunk) {
+  return (uint32_t)head * 512u + 16u * (uint32_t)(chunk ^ head);
 }
 
-// Merge the NW waves of the workgroup and emit the output or a partial.
-template <int NW>
-__device__ __forceinline__ void finish_block(const AttnCommon& P, WaveState& st, float* smem,
-                                             int64_t pair, int split, int lane, int wave) {
-  float* sh_m = smem;                       // [NW][16]
-  float* sh_l = smem + NW * kMaxGroup;      // [NW][16]
-  float* sh_o = smem + 2 * NW * kMaxGroup;  // [NW][G][kORow]
-
+__device__ __forceinline__ void publish_ml(const AttnCommon& P, WaveState& st, char* lds, int lane,
+                                           int wave) {
   st.l += __shfl_xor(st.l, 16);
   st.l += __shfl_xor(st.l, 32);
   const int n = lane & 15, g = lane >> 4;
-  if (n < P.G) {
-    if (g == 0) {
-      sh_m[wave * kMaxGroup + n] = st.m;
-      sh_l[wave * kMaxGroup + n] = st.l;
-    }
-    float* orow = sh_o + ((size_t)wave * P.G + n) * kORow + 32 * g;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) orow[8 * r + jj] = st.O[jj][r];
+  if (n < P.G && g == 0) {
+    reinterpret_cast<float*>(lds + kLdsM)[wave * kMaxGroup + n] = st.m;
+    reinterpret_cast<float*>(lds + kLdsL)[wave * kMaxGroup + n] = st.l;
   }
-  __syncthreads();
+}
 
+// fp16-tile accumulators: O[jj][r] is channel 8(4g + r) + jj of head n.
+__device__ __forceinline__ void publish_f(const AttnCommon& P, const WaveState& st, char* slot,
+                                          int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  if (n < P.G) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c0 = 2 * (4 * g + r);
+      float4v lo = {st.O[0][r], st.O[1][r], st.O[2][r], st.O[3][r]};
+      float4v hi = {st.O[4][r], st.O[5][r], st.O[6][r], st.O[7][r]};
+      *reinterpret_cast<float4v*>(slot + row_off(n, c0)) = lo;
+      *reinterpret_cast<float4v*>(slot + row_off(n, c0 + 1)) = hi;
+    }
+  }
+}
+
+// Quantized-tile accumulators: lane (t, g) holds head 4g + r, channel
+// 16 blk + t.  ADD: the slot already holds this wave's fp16-tile rows.
+template <bool ADD>
+__device__ __forceinline__ void publish_q(QState& qs, char* slot, char* tmp, int lane) {
+  q_state_rows(qs, tmp, lane);
+  const int t = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = 4 * g + r;
+      float* p = reinterpret_cast<float*>(slot + row_off(h, 4 * blk + (t >> 2)) + 4 * (t & 3));
+      *p = ADD ? *p + qs.O[blk][r] : qs.O[blk][r];
+    }
+}
+
+// Barrier, then combine the waves' published partials into the output (one
+// split) or the split's fp32 partial.
+__device__ __forceinline__ void merge_out(const AttnCommon& P, char* lds, int64_t pair, int split) {
+  __syncthreads();
+  const float* sh_m = reinterpret_cast<const float*>(lds + kLdsM);
+  const float* sh_l = reinterpret_cast<const float*>(lds + kLdsL);
   const int64_t b = pair / P.KVH;
   const int kvh = (int)(pair % P.KVH);
   const size_t total = (size_t)P.pairs * P.n_splits * P.G;
-  for (int e = threadIdx.x; e < P.G * kHeadDim; e += 64 * NW) {
-    const int hn = e / kHeadDim, d = e % kHeadDim;
+  // One thread per (head, 4-channel chunk).
+  for (int e = threadIdx.x; e < P.G * 32; e += kThreads) {
+    const int hn = e >> 5, ch = e & 31;
     float M = kMaxSentinel;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, sh_m[w * kMaxGroup + hn]);
-    float L = 0.f, acc = 0.f;
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sh_m[w * kMaxGroup + hn]);
+    float L = 0.f;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
+    for (int w = 0; w < kWaves; ++w) {
       const float f = __builtin_amdgcn_exp2f(sh_m[w * kMaxGroup + hn] - M);
       L += sh_l[w * kMaxGroup + hn] * f;
-      acc += sh_o[((size_t)w * P.G + hn) * kORow + d] * f;
+      const float4v o =
+          *reinterpret_cast<const float4v*>(lds + kLdsSlots + w * kSlotBytes + row_off(hn, ch));
+      acc += o * f;
     }
     if (P.n_splits == 1) {
-      P.o[((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + d] = (_Float16)(acc / L);
+      const float inv = 1.0f / L;
+      half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
+                  (_Float16)(acc[3] * inv)};
+      *reinterpret_cast<half4v*>(P.o + ((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim +
+                                 4 * ch) = h;
     } else {
       const size_t idx = ((size_t)pair * P.n_splits + split) * P.G + hn;
-      P.ws[idx * kHeadDim + d] = acc;
-      if (d == 0) {
+      *reinterpret_cast<float4v*>(P.ws + idx * kHeadDim + 4 * ch) = acc;
+      if (ch == 0) {
         P.ws[total * kHeadDim + idx] = M;
         P.ws[total * kHeadDim + total + idx] = L;
       }
@@ -105,45 +261,44 @@ __device__ __forceinline__ void finish_block(const AttnCommon& P, WaveState& st,
   }
 }
 
-// Stream fp16 tiles [tb, te) of one region through the wave, two tiles in
-// flight (ping-pong register buffers).  Row r of the region is slot
-// slot_base + r.
-__device__ __forceinline__ void run_f16_tiles(const _Float16* __restrict__ kb,
-                                              const _Float16* __restrict__ vb, int rows,
-                                              int slot_base, int tb, int te,
-                                              const half8 (&qB)[4], const AttnCommon& P,
-                                              WaveState& st, int lane) {
-  if (tb >= te) return;
-  Tile A, B;
-  load_f16_tile(kb, vb, kTile * tb, rows, lane, A);
-  for (int ti = tb; ti < te; ti += 2) {
-    if (ti + 1 < te) load_f16_tile(kb, vb, kTile * (ti + 1), rows, lane, B);
-    tile_step(A, qB, slot_base + kTile * ti, P.R, P.scale_log2, st, lane);
-    if (ti + 1 >= te) break;
-    if (ti + 2 < te) load_f16_tile(kb, vb, kTile * (ti + 2), rows, lane, A);
-    tile_step(B, qB, slot_base + kTile * (ti + 1), P.R, P.scale_log2, st, lane);
-  }
-}
-
 // fp16 rows: the dense cache [B, KVH, L, 128] or the compacted sparse cache
 // [B, KVH, sink+window, 128]; slot == row.
 struct F16Src {
-  static constexpr bool kQuant = false;
   const _Float16* k;
   const _Float16* v;
   int rows;
-  __device__ __forceinline__ void run(int64_t pair, int wb, int we, const half8 (&qB)[4],
-                                      const AttnCommon& P, WaveState& st, char*, int lane) const {
+
+  __device__ __forceinline__ void init_counters(int* ctr) const { ctr[0] = 2 * kWaves; }
+
+  // Issue the wave's first loads, then `sync` (workgroup barrier when the
+  // queue is dynamic; fills the step context), then stream the queue.
+  template <class Sync>
+  __device__ __forceinline__ void process(int64_t pair, int split, const AttnCommon& P, int wave,
+                                          int lane, int* ctr, Sync&& sync, WaveState& st) const {
+    F16Items it;
     const size_t off = (size_t)pair * rows * kHeadDim;
-    run_f16_tiles(k + off, v + off, rows, 0, wb, we, qB, P, st, lane);
+    const uint32_t bytes = (uint32_t)rows * kRowBytes;
+    it.rk = make_rsrc(k + off, bytes);
+    it.rv = make_rsrc(v + off, bytes);
+    it.tile0 = split * P.tiles_per_split;
+    it.n = min(P.tiles_per_split, P.n_tiles - it.tile0);
+    it.slot_base = 0;
+    Ring<F16Items> ring;
+    ring_begin(it, ring, wave, wave + kWaves, lane);
+    StepCtx c;
+    sync(c, it.n > 2 * kWaves);
+    if (it.n > 2 * kWaves)
+      ring_run_dynamic(it, ring, ctr, st, c);
+    else
+      ring_run_static(it, ring, st, c);
+    publish_ml(P, st, c.lds, lane, wave);
+    publish_f(P, st, c.slot, lane);
   }
 };
 
-// KIVI cache: tile 0 = the sink group (quantized, `sink` real tokens), tiles
-// 1..nwt = window-old groups (quantized), then the fp16 residual tiles.
+// KIVI cache: the fp16 residual (slots sink + win_tok ..) and the quantized
+// sink and window-old groups.
 struct KiviSrc {
-  static constexpr bool kQuant = true;
-  static constexpr int kRing = 3;   // quantized tiles in flight per wave
   const _Float16* kres;
   const _Float16* vres;
   int res_rows;
@@ -153,86 +308,175 @@ struct KiviSrc {
   int win_tok;     // window - residual
   int nwt;         // win_tok / 32
 
-  __device__ __forceinline__ void run(int64_t pair, int wb, int we, const half8 (&qB)[4],
-                                      const AttnCommon& P, WaveState& st, char* slot,
-                                      int lane) const {
-    const int nq = 1 + nwt;
-    const int qb = wb, qe = we < nq ? we : nq;
-    if (qb < qe) {
-      QRegion S = sinkq, W = winq;
-      S.kp += (size_t)pair * 8 * kHeadDim;
-      S.ks += (size_t)pair * kHeadDim;
-      S.kz += (size_t)pair * kHeadDim;
-      S.vp += (size_t)pair * 32 * 32;
-      S.vs += (size_t)pair * 32 * 4;
-      S.vz += (size_t)pair * 32 * 4;
-      if (nwt > 0) {
-        W.kp += (size_t)pair * (win_tok / 4) * kHeadDim;
-        W.ks += (size_t)pair * (win_tok / 32) * kHeadDim;
-        W.kz += (size_t)pair * (win_tok / 32) * kHeadDim;
-        W.vp += (size_t)pair * win_tok * 32;
-        W.vs += (size_t)pair * win_tok * 4;
-        W.vz += (size_t)pair * win_tok * 4;
-      }
-      // tile ti: 0 = sink group (slots 0..sink-1), else window-old group ti-1
-      auto load = [&](int ti, QTileRaw& X) {
-        if (ti == 0)
-          load_q_raw(S, 0, lane, X);
+  // Work split.  While the residual has at most kWaves tiles, the first nrw
+  // waves take one residual tile each and the other nqw waves are quantized
+  // waves.  The quantized queue is served in this order: one tile per
+  // quantized wave, one extra tile per residual wave, a second tile per
+  // quantized wave (all three loaded at launch), then dynamically.  A longer
+  // residual makes every wave a residual wave with a dynamic residual queue,
+  // and all quantized tiles dynamic.
+  __device__ __forceinline__ int n_res() const { return res_rows / kTile; }
+  __device__ __forceinline__ int n_res_waves() const { return min(n_res(), kWaves); }
+  __device__ __forceinline__ int n_static_q() const {
+    const int nrw = n_res_waves(), nqw = kWaves - nrw;
+    return nqw == 0 ? 0 : 2 * nqw + nrw;
+  }
+
+  __device__ __forceinline__ void init_counters(int* ctr) const {
+    ctr[0] = 2 * n_res_waves();
+    ctr[1] = n_static_q();
+  }
+
+  // Residual waves and quantized waves run separate straight-line programs
+  // (each issues its first loads, then `sync`, then streams), so the two
+  // prefetch rings are never live at the same time.
+  template <class Sync>
+  __device__ __forceinline__ void process(int64_t pair, int, const AttnCommon& P, int wave,
+                                          int lane, int* ctr, Sync&& sync, WaveState& st) const {
+    const int nrw = n_res_waves();
+    QRegion S = sinkq, Wq = winq;
+    S.kp += (size_t)pair * 8 * kHeadDim;
+    S.ks += (size_t)pair * kHeadDim;
+    S.kz += (size_t)pair * kHeadDim;
+    S.vp += (size_t)pair * 32 * 32;
+    S.vs += (size_t)pair * 32 * 4;
+    S.vz += (size_t)pair * 32 * 4;
+    if (nwt > 0) {
+      Wq.kp += (size_t)pair * (win_tok / 4) * kHeadDim;
+      Wq.ks += (size_t)pair * (win_tok / 32) * kHeadDim;
+      Wq.kz += (size_t)pair * (win_tok / 32) * kHeadDim;
+      Wq.vp += (size_t)pair * win_tok * 32;
+      Wq.vs += (size_t)pair * win_tok * 4;
+      Wq.vz += (size_t)pair * win_tok * 4;
+    }
+    QItems<true> qit;   // tiles of a wave that also holds fp16-tile accumulators
+    qit.sinkq = S;
+    qit.winq = Wq;
+    qit.n = 1 + nwt;
+    qit.sink = sink;
+    QItems<false> qonly;
+    qonly.sinkq = S;
+    qonly.winq = Wq;
+    qonly.n = 1 + nwt;
+    qonly.sink = sink;
+    QState qs;
+    q_state_init(qs);
+    QRef qref{st, qs};
+    const int nqw = kWaves - nrw;
+    const bool dyn_q = qit.n > n_static_q();
+    const bool dyn = dyn_q || (nqw == 0 && n_res() > 2 * nrw);   // any dynamic queue
+#if KVDEC_RES_FIRST
+    const int rw = wave, qw = wave - nrw;
+#else
+    const int rw = wave - nqw, qw = wave;
+#endif
+    StepCtx c;
+    if (rw >= 0 && rw < nrw) {
+      F16Items rit;
+      const size_t roff = (size_t)pair * res_rows * kHeadDim;
+      const uint32_t rbytes = (uint32_t)res_rows * kRowBytes;
+      rit.rk = make_rsrc(kres + roff, rbytes);
+      rit.rv = make_rsrc(vres + roff, rbytes);
+      rit.tile0 = 0;
+      rit.n = n_res();
+      rit.slot_base = sink + win_tok;
+      bool has_q = false;
+      if (nqw > 0) {
+        // one residual tile and (if there is one) one extra quantized tile
+        F16Raw R;
+        QTileRaw E;
+        rit.load(rw, R, lane);
+        const int qe = nqw + rw;
+        qit.load(qe, E, lane);
+        sync(c, dyn);
+        rit.step(rw, R, st, c);
+        if (qe < qit.n) {
+          qit.step(qe, E, qref, c);
+          has_q = true;
+        }
+      } else {
+        Ring<F16Items> rring;
+        ring_begin(rit, rring, rw, rw + nrw, lane);
+        sync(c, dyn);
+        if (rit.n > 2 * nrw)
+          ring_run_dynamic(rit, rring, ctr, st, c);
         else
-          load_q_raw(W, ti - 1, lane, X);
-      };
-      // Ring of kRing raw tiles in flight; each is staged through the wave's
-      // LDS slot into operand layout just before it is consumed.
-      QTileRaw ring[kRing];
-#pragma unroll
-      for (int k = 0; k < kRing; ++k)
-        if (qb + k < qe) load(qb + k, ring[k]);
-      for (int base = qb; base < qe; base += kRing) {
-#pragma unroll
-        for (int k = 0; k < kRing; ++k) {
-          const int ti = base + k;
-          if (ti < qe) {
-            stage_q_raw(ring[k], slot, lane);
-            if (ti + kRing < qe) load(ti + kRing, ring[k]);
-            q_tile_step(slot, qB, ti == 0 ? 0 : sink + kTile * (ti - 1), ti == 0 ? sink : kTile,
-                        P.R, P.scale_log2, st, lane);
-          }
+          ring_run_static(rit, rring, st, c);
+      }
+      if (dyn_q) {
+        const int s0 = grab(ctr + 1, lane);
+        const int s1 = grab(ctr + 1, lane);
+        if (s0 < qit.n) {
+          Ring<QItems<true>> qring;
+          ring_begin(qit, qring, s0, s1, lane);
+          ring_run_dynamic(qit, qring, ctr + 1, qref, c);
+          has_q = true;
         }
       }
-    }
-    const int fb = (wb > nq ? wb : nq) - nq, fe = we - nq;
-    if (fb < fe) {
-      const size_t off = (size_t)pair * res_rows * kHeadDim;
-      run_f16_tiles(kres + off, vres + off, res_rows, sink + win_tok, fb, fe, qB, P, st, lane);
+      publish_ml(P, st, c.lds, lane, wave);
+      publish_f(P, st, c.slot, lane);
+      if (has_q) publish_q<true>(qs, c.slot, c.lds + kLdsTmp + wave * 256, lane);
+    } else {
+      Ring<QItems<false>> qring;
+      ring_begin(qonly, qring, qw, qw + nqw + nrw, lane);
+      sync(c, dyn);
+      if (dyn_q)
+        ring_run_dynamic(qonly, qring, ctr + 1, qref, c);
+      else
+        ring_run_static(qonly, qring, qref, c);
+      publish_ml(P, st, c.lds, lane, wave);
+      publish_q<false>(qs, c.slot, c.lds + kLdsTmp + wave * 256, lane);
     }
   }
 };
 
-// NW waves per workgroup, two waves per SIMD.
-template <class Src, int NW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnCommon P, Src S) {
-  extern __shared__ float smem[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+template <class Src>
+__global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) {
+  extern __shared__ __align__(16) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int split = (int)(blockIdx.x % (unsigned)P.n_splits);
   const int64_t pair = blockIdx.x / (unsigned)P.n_splits;
   const int64_t b = pair / P.KVH;
   const int kvh = (int)(pair % P.KVH);
 
+  // Q operand of this KV head's G query heads, loaded by every wave straight
+  // into MFMA B-operand order (lane (n, g): head n, channels 32c + 8g .. +7)
+  // before any tile load, so no wave waits on another to start computing.
   half8 qB[4];
-  load_q_operand(P, b, kvh, lane, qB);
+  {
+    const int n = lane & 15, g = lane >> 4;
+    const u32x4* qp = reinterpret_cast<const u32x4*>(
+                          P.q + ((size_t)b * P.H + (size_t)kvh * P.G + min(n, P.G - 1)) * kHeadDim) + g;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const u32x4 v = qp[4 * cc];
+      qB[cc] = as_h8(n < P.G ? v : u32x4{0u, 0u, 0u, 0u});
+    }
+  }
 
-  const int t0 = split * P.tiles_per_split;
-  const int t1 = min(t0 + P.tiles_per_split, P.n_tiles);
-  const int nt = t1 - t0;
-  const int wb = t0 + (nt * wave) / NW;
-  const int we = t0 + (nt * (wave + 1)) / NW;
+  int* ctr = reinterpret_cast<int*>(lds + kLdsCtr);
+  // Called exactly once by every wave, after its first tile loads.  With a
+  // dynamic work queue (`barrier`, the same for every wave of the
+  // workgroup) the counters are set and the workgroup synchronises.
+  auto sync = [&](StepCtx& c, bool barrier) {
+    if (barrier) {
+      if (threadIdx.x == 0) S.init_counters(ctr);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) c.qB[cc] = qB[cc];
+    c.scale_log2 = P.scale_log2;
+    c.R = P.R;
+    c.lds = lds;
+    c.slot = lds + kLdsSlots + wave * kSlotBytes;
+    c.lane = lane;
+  };
 
   WaveState st;
   wave_state_init(st);
-  char* slot = reinterpret_cast<char*>(smem) + (size_t)wave * kQSlotBytes;
-  S.run(pair, wb, we, qB, P, st, slot, lane);
-  finish_block<NW>(P, st, smem + stage_lds_bytes(NW, Src::kQuant) / sizeof(float), pair, split,
-                   lane, wave);
+  S.process(pair, split, P, wave, lane, ctr, sync, st);
+  merge_out(P, lds, pair, split);
 }
 
 // Log-sum-exp merge of the split partials: one thread per output element.
@@ -266,28 +510,24 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnCommon P) {
 // Host side
 // ---------------------------------------------------------------------------
 
-// Launch plan.  Aim for kTargetWaves resident waves over the whole chip (256
-// CUs x 2 waves per SIMD x 4 SIMDs), at least kMinTilesPerWave tiles each; a
-// KV head gets up to 8 waves in one workgroup and more waves only through
-// splits (which need the merge pass).
-constexpr int64_t kTargetWaves = 2048;
-constexpr int64_t kMinTilesPerWave = 2;
+// Launch plan: one workgroup per (KV head, split).  Splits are added only
+// while there are fewer work units than CUs (kTargetUnits), and only while
+// every unit keeps at least one tile per wave.
+constexpr int64_t kTargetUnits = 256;
+constexpr int64_t kMinTilesPerUnit = kWaves;
 
 struct Plan {
-  int nw, splits, tps;
+  int splits, tps;
 };
 
-Plan make_plan(int64_t pairs, int64_t n_tiles, int G, bool quant) {
-  int64_t wpp = (kTargetWaves + pairs - 1) / pairs;
-  const int64_t cap = (n_tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
-  if (wpp > cap) wpp = cap;
-  if (wpp < 1) wpp = 1;
-  const bool fits8 = merge_lds_bytes(8, G) + stage_lds_bytes(8, quant) <= 65536;
-  Plan p;
-  p.nw = (wpp > 4 && fits8) ? 8 : 4;
-  int64_t s = (wpp + p.nw - 1) / p.nw;
+Plan make_plan(int64_t pairs, int64_t n_tiles) {
+  int64_t s = (kTargetUnits + pairs - 1) / pairs;
+  const int64_t cap = n_tiles / kMinTilesPerUnit;
+  if (s > cap) s = cap;
+  if (s < 1) s = 1;
   int64_t t = (n_tiles + s - 1) / s;
   s = (n_tiles + t - 1) / t;
+  Plan p;
   p.splits = (int)s;
   p.tps = (int)t;
   return p;
@@ -317,8 +557,10 @@ int launch_status() {
 }
 
 template <class Src>
-int launch_attn(AttnCommon P, const Src& S, size_t ws_bytes, hipStream_t stream) {
-  const Plan plan = make_plan(P.pairs, P.n_tiles, P.G, Src::kQuant);
+int launch_attn(AttnCommon P, const Src& S, bool kivi, size_t ws_bytes, hipStream_t stream) {
+  // The KIVI plan never splits: its quantized and residual regions are
+  // addressed per KV head, and the windows it serves are short.
+  const Plan plan = kivi ? Plan{1, P.n_tiles} : make_plan(P.pairs, P.n_tiles);
   P.n_splits = plan.splits;
   P.tiles_per_split = plan.tps;
   if (plan.splits > 1) {
@@ -327,13 +569,8 @@ int launch_attn(AttnCommon P, const Src& S, size_t ws_bytes, hipStream_t stream)
   }
   const int64_t blocks = P.pairs * plan.splits;
   if (blocks > 0x7fffffffLL) return KVDEC_E_SHAPE;
-  const size_t lds = stage_lds_bytes(plan.nw, Src::kQuant) + merge_lds_bytes(plan.nw, P.G);
-  if (plan.nw == 8)
-    hipLaunchKernelGGL((attn_kernel<Src, 8>), dim3((unsigned)blocks), dim3(64 * 8), lds, stream,
-                       P, S);
-  else
-    hipLaunchKernelGGL((attn_kernel<Src, 4>), dim3((unsigned)blocks), dim3(64 * 4), lds, stream,
-                       P, S);
+  hipLaunchKernelGGL((attn_kernel<Src>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream,
+                     P, S);
   int rc = launch_status();
   if (rc != KVDEC_OK || plan.splits == 1) return rc;
   const int64_t outs = P.pairs * P.G * kHeadDim;
@@ -385,19 +622,19 @@ const char* kvdec_strerror(int code) {
   return "unknown kvdec error";
 }
 
-const char* kvdec_version(void) { return "kvdec 0.2 gfx950"; }
+const char* kvdec_version(void) { return "kvdec 0.3 gfx950"; }
 
 int kvdec_num_splits(int kind, int64_t B, int32_t KVH, int64_t n_slots) {
   if (B < 1 || KVH < 1 || n_slots < 1) return 1;
-  // The plan's split count does not depend on the group size, only the
-  // waves-per-workgroup choice does.
-  return make_plan(B * KVH, tiles_for(kind, n_slots), 8, kind == KVDEC_KIND_KIVI).splits;
+  if (kind == KVDEC_KIND_KIVI) return 1;
+  return make_plan(B * KVH, tiles_for(kind, n_slots)).splits;
 }
 
 size_t kvdec_workspace_bytes(int kind, int64_t B, int32_t H, int32_t KVH, int64_t n_slots,
                              int32_t D) {
   if (check_heads(B, H, KVH, D) != KVDEC_OK || n_slots < 1) return 0;
-  const Plan p = make_plan(B * KVH, tiles_for(kind, n_slots), H / KVH, kind == KVDEC_KIND_KIVI);
+  if (kind == KVDEC_KIND_KIVI) return 0;
+  const Plan p = make_plan(B * KVH, tiles_for(kind, n_slots));
   return ws_bytes_for(B * KVH, p.splits, H / KVH);
 }
 
@@ -409,7 +646,7 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int
   int rc = check_heads(B, H, KVH, D);
   if (rc) return rc;
   if (L < 1) return KVDEC_E_SEQLEN;
-  if (L * kHeadDim * 2 >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;   // 32-bit in-head offsets
+  if (L * kRowBytes >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;   // 32-bit in-head offsets
   AttnCommon P{};
   P.q = static_cast<const _Float16*>(q);
   P.o = static_cast<_Float16*>(o);
@@ -422,7 +659,7 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int
   P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
   P.R = SlotRanges{(int)L, 0, 0};
   F16Src S{static_cast<const _Float16*>(k), static_cast<const _Float16*>(v), (int)L};
-  return launch_attn(P, S, ws_bytes, static_cast<hipStream_t>(stream));
+  return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache, void* o,
@@ -438,7 +675,7 @@ int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
   if (layout != KVDEC_LAYOUT_LINEAR && layout != KVDEC_LAYOUT_RING) return KVDEC_E_UNSUPPORTED;
   if (layout == KVDEC_LAYOUT_RING && window < 1) return KVDEC_E_WINDOW;
   const int64_t n = (int64_t)window + sink;
-  if (n * kHeadDim * 2 >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;
+  if (n * kRowBytes >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;
   AttnCommon P{};
   P.q = static_cast<const _Float16*>(q);
   P.o = static_cast<_Float16*>(o);
@@ -451,7 +688,7 @@ int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
   P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
   P.R = sparse_ranges(seq_len, window, sink, layout);
   F16Src S{static_cast<const _Float16*>(k_cache), static_cast<const _Float16*>(v_cache), (int)n};
-  return launch_attn(P, S, ws_bytes, static_cast<hipStream_t>(stream));
+  return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res,
@@ -474,14 +711,16 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
   if (win_tok > 0)
     for (int i = 6; i < 12; ++i)
       if (!kivi[i]) return KVDEC_E_NULL;
-  if ((int64_t)residual * kHeadDim * 2 >= ((int64_t)1 << 31) ||
+  if ((int64_t)residual * kRowBytes >= ((int64_t)1 << 31) ||
       (int64_t)win_tok * kHeadDim >= ((int64_t)1 << 31))
     return KVDEC_E_SHAPE;
+  (void)ws;
+  (void)ws_bytes;
 
   AttnCommon P{};
   P.q = static_cast<const _Float16*>(q);
   P.o = static_cast<_Float16*>(o);
-  P.ws = static_cast<float*>(ws);
+  P.ws = nullptr;
   P.pairs = B * KVH;
   P.H = H;
   P.KVH = KVH;
@@ -504,7 +743,7 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
   S.sink = sink;
   S.win_tok = win_tok;
   S.nwt = win_tok / kTile;
-  return launch_attn(P, S, ws_bytes, static_cast<hipStream_t>(stream));
+  return launch_attn(P, S, true, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

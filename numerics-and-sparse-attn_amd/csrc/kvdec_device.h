@@ -12,6 +12,16 @@
 //        tokens whose probabilities the same lane holds after QK.
 // The GQA group (<= 16 query heads sharing one KV head) fills the 16 MFMA
 // columns, so every K/V byte is read from HBM once per KV head.
+//
+// Memory access: every cache read is a raw buffer load against a resource
+// that covers exactly the bytes of one region of one KV head.  A load past
+// the region (the rows of a partial last tile, or the dummy loads a wave
+// issues once its work queue is empty) returns zeros without touching
+// memory, so a stream issues the same instructions whatever its state and
+// the compiler's memory-counter waits stay exact across the prefetch ring.
+// Every instruction of an fp16 tile reads 4 whole 256-byte rows (K) or 4
+// whole rows (V); K is transposed into MFMA operand order through the wave's
+// LDS slot.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -20,17 +30,50 @@
 namespace kvdec {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kHeadDim = 128;   // D: fixed by the MFMA tiling below
-constexpr int kTile = 32;       // tokens per tile (one KIVI group)
-constexpr int kMaxGroup = 16;   // query heads per KV head (MFMA columns)
+constexpr int kHeadDim = 128;               // D: fixed by the MFMA tiling below
+constexpr int kRowBytes = kHeadDim * 2;     // one fp16 K or V row
+constexpr int kTile = 32;                   // tokens per tile (one KIVI group)
+constexpr int kMaxGroup = 16;               // query heads per KV head (MFMA columns)
+constexpr int kSlotBytes = kTile * kRowBytes;   // per-wave LDS slot: one K tile
+constexpr uint32_t kOOB = 0x80000000u;      // buffer offset past every region
+
+// Cache policy of the streaming K/V/code loads: non-temporal (read once per
+// step; keeps them from displacing the caches' dirty lines).
+#ifndef KVDEC_STREAM_AUX
+#define KVDEC_STREAM_AUX 2
+#endif
+constexpr int kStreamAux = KVDEC_STREAM_AUX;
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw (unstructured) buffer resource over `bytes` bytes at `base`.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kStreamAux);
+}
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kStreamAux);
+}
 
 __device__ __forceinline__ half8 as_h8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 __device__ __forceinline__ u32x4 as_u4(half8 v) { return __builtin_bit_cast(u32x4, v); }
+
+// a - b on two fp16 lanes in one v_pk_add_f16 (with negated b); written out
+// because the compiler splits fp16 vector subtraction into scalar halves.
+__device__ __forceinline__ uint32_t pk_sub_f16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_add_f16 %0, %1, %2 neg_lo:[0,1] neg_hi:[0,1]" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 
 __device__ __forceinline__ float4v mfma16x16x32(u32x4 a, half8 b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(a), b, c, 0, 0, 0);
@@ -169,49 +212,50 @@ __device__ __forceinline__ void tile_body(KOp&& kop, VOp&& vop, uint32_t valid,
 // fp16 tiles
 // ---------------------------------------------------------------------------
 
-// One 32-token fp16 tile in MFMA operand layout:
-//   k[blk][c] : K[token 16*blk + t][channels 32c + 8g .. +7]
-//   v[j]      : V[token tau(g, j)][channels 8m .. 8m+7]
-struct Tile {
-  u32x4 k[2][4];
+// One 32-token fp16 tile as loaded:
+//   k[i] : K[row 4i + g][channels 8t .. 8t+7]     (whole rows per instruction)
+//   v[j] : V[row tau(g, j)][channels 8t .. 8t+7]  (V operand order after perm)
+struct F16Raw {
+  u32x4 k[8];
   u32x4 v[8];
 };
 
-// Consume an fp16 tile.  V rows of masked tokens are replaced by zeros at use
-// time: unwritten cache slots may hold anything, including non-finite values.
-__device__ __forceinline__ void tile_step(const Tile& T, const half8 (&qB)[4], int slot0,
-                                          const SlotRanges& R, float scale_log2, WaveState& st,
-                                          int lane) {
-  auto kop = [&](int blk, int c) { return T.k[blk][c]; };
-  if (tile_fully_valid(R, slot0)) {
-    tile_body<true>(kop, [&](int w, int j) { return T.v[j][w]; }, 0u, qB, scale_log2, st);
-  } else {
-    const uint32_t valid = tile_valid_bits(R, slot0, kTile, lane);
-    tile_body<false>(kop, [&](int w, int j) { return ((valid >> j) & 1u) ? T.v[j][w] : 0u; },
-                     valid, qB, scale_log2, st);
-  }
+// Issue the loads of the tile whose first row sits at byte `base` of the
+// region (kOOB: no tile, every load returns zeros without a memory access).
+__device__ __forceinline__ void load_f16(rsrc_t rk, rsrc_t rv, uint32_t base, int lane,
+                                         F16Raw& X) {
+  const uint32_t t = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) X.k[i] = bload16(rk, base + (4u * i + g) * kRowBytes + 16u * t);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) X.v[j] = bload16(rv, base + (uint32_t)tau(g, j) * kRowBytes + 16u * t);
 }
 
-// Load an fp16 tile from a [rows, 128] region (one KV head, base pointers
-// uniform across the wave).  Rows past the end are clamped to the last row;
-// their slots are invalid, so tile_step masks them.
-__device__ __forceinline__ void load_f16_tile(const _Float16* __restrict__ kb,
-                                              const _Float16* __restrict__ vb, int row0,
-                                              int rows, int lane, Tile& T) {
-  const int t = lane & 15, g = lane >> 4;
-  const char* kc = reinterpret_cast<const char*>(kb);
-  const char* vc = reinterpret_cast<const char*>(vb);
+// LDS byte offset of 16-byte chunk `chunk` of K row `row` inside a wave slot:
+// chunks are XOR-swizzled by the row so that both the row-wise stores and
+// the column-wise MFMA operand reads hit 16 distinct bank groups.
+__device__ __forceinline__ uint32_t kslot_off(uint32_t row, uint32_t chunk) {
+  return row * kRowBytes + 16u * (chunk ^ (row & 15u));
+}
+
+// Consume an fp16 tile.  V rows of masked tokens are replaced by zeros at use
+// time: unwritten cache slots may hold anything, including non-finite values.
+__device__ __forceinline__ void f16_tile_step(const F16Raw& X, char* slot, const half8 (&qB)[4],
+                                              int slot0, const SlotRanges& R, float scale_log2,
+                                              WaveState& st, int lane) {
+  const uint32_t t = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int blk = 0; blk < 2; ++blk) {
-    const int r = min(row0 + 16 * blk + t, rows - 1);
-    const uint32_t off = (uint32_t)r * (kHeadDim * 2) + 16u * g;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) T.k[blk][c] = *reinterpret_cast<const u32x4*>(kc + off + 64u * c);
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int r = min(row0 + tau(g, j), rows - 1);
-    T.v[j] = *reinterpret_cast<const u32x4*>(vc + (uint32_t)r * (kHeadDim * 2) + 16u * t);
+  for (int i = 0; i < 8; ++i)
+    *reinterpret_cast<u32x4*>(slot + kslot_off(4u * i + g, t)) = X.k[i];
+  auto kop = [&](int blk, int c) {
+    return *reinterpret_cast<const u32x4*>(slot + kslot_off(16u * blk + t, 4u * c + g));
+  };
+  if (tile_fully_valid(R, slot0)) {
+    tile_body<true>(kop, [&](int w, int j) { return X.v[j][w]; }, 0u, qB, scale_log2, st);
+  } else {
+    const uint32_t valid = tile_valid_bits(R, slot0, kTile, lane);
+    tile_body<false>(kop, [&](int w, int j) { return ((valid >> j) & 1u) ? X.v[j][w] : 0u; },
+                     valid, qB, scale_log2, st);
   }
 }
 
@@ -219,10 +263,10 @@ __device__ __forceinline__ void load_f16_tile(const _Float16* __restrict__ kb,
 // KIVI 2-bit tiles
 // ---------------------------------------------------------------------------
 
-// Device pointers of one KIVI-quantized region, bound to one KV head.  A
-// 32-token tile tq is one quantization group: 1 KB of K codes (8 byte rows of
-// 128 channels), 128 K scales and zeros, 1 KB of V codes (32 tokens x 32
-// bytes), 32 x 4 V scales and zeros -- six contiguous pieces.
+// Device pointers of one KIVI-quantized region of one KV head.  A 32-token
+// tile tq is one quantization group: 1 KB of K codes (8 byte rows of 128
+// channels), 128 K scales and zeros, 1 KB of V codes (32 tokens x 32 bytes),
+// 32 x 4 V scales and zeros -- six contiguous pieces.
 struct QRegion {
   const uint8_t* kp;     // [ntok/4][128]
   const _Float16* ks;    // [ntok/32][128]
@@ -232,8 +276,8 @@ struct QRegion {
   const _Float16* vz;
 };
 
-// A tile as loaded from HBM: every lane fetches a 1/64 slice of each piece
-// with one coalesced load (12 VGPRs per tile, no duplication across lanes).
+// A tile as loaded: every lane fetches a 1/64 slice of each piece with one
+// coalesced load (12 VGPRs per tile, no duplication across lanes).
 struct QTileRaw {
   u32x4 kc;            // K code bytes [16L, 16L+16)
   u32x4 vc;            // V code bytes [16L, 16L+16)
@@ -241,110 +285,233 @@ struct QTileRaw {
   uint32_t vs, vz;     // V scale / zero of token L/2, groups 2(L%2), 2(L%2)+1
 };
 
-__device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, int lane, QTileRaw& X) {
-  X.kc = *reinterpret_cast<const u32x4*>(Q.kp + (size_t)tq * 1024 + 16 * lane);
-  X.vc = *reinterpret_cast<const u32x4*>(Q.vp + (size_t)tq * 1024 + 16 * lane);
-  X.ks = *reinterpret_cast<const uint32_t*>(Q.ks + (size_t)tq * kHeadDim + 2 * lane);
-  X.kz = *reinterpret_cast<const uint32_t*>(Q.kz + (size_t)tq * kHeadDim + 2 * lane);
-  X.vs = *reinterpret_cast<const uint32_t*>(Q.vs + (size_t)tq * 128 + 2 * lane);
-  X.vz = *reinterpret_cast<const uint32_t*>(Q.vz + (size_t)tq * 128 + 2 * lane);
+// Issue the loads of tile tq of region Q (valid == false: zeros, no access).
+__device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, bool valid, int lane,
+                                           QTileRaw& X) {
+  const size_t t = valid ? (size_t)tq : 0;
+  const uint32_t n16 = valid ? 1024u : 0u, n4 = valid ? 256u : 0u;
+  X.kc = bload16(make_rsrc(Q.kp + t * 1024, n16), 16u * lane);
+  X.vc = bload16(make_rsrc(Q.vp + t * 1024, n16), 16u * lane);
+  X.ks = bload4(make_rsrc(Q.ks + t * kHeadDim, n4), 4u * lane);
+  X.kz = bload4(make_rsrc(Q.kz + t * kHeadDim, n4), 4u * lane);
+  X.vs = bload4(make_rsrc(Q.vs + t * 128, n4), 4u * lane);
+  X.vz = bload4(make_rsrc(Q.vz + t * 128, n4), 4u * lane);
 }
 
-// Per-wave LDS staging slot of one tile (bytes): K codes [0,1024), K scales
-// [1024,1280), K zeros [1280,1536), V codes [1536,2560), V (scale, zero)
-// pairs [2560,3072) at 2560 + 16*token + 4*group.
-constexpr int kQSlotBytes = 3072;
-
-__device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
-  *reinterpret_cast<u32x4*>(slot + 16 * lane) = X.kc;
-  *reinterpret_cast<uint32_t*>(slot + 1024 + 4 * lane) = X.ks;
-  *reinterpret_cast<uint32_t*>(slot + 1280 + 4 * lane) = X.kz;
-  *reinterpret_cast<u32x4*>(slot + 1536 + 16 * lane) = X.vc;
-  u32x2 sz;
-  sz[0] = __builtin_amdgcn_perm(X.vz, X.vs, 0x05040100u);   // (scale, zero) of group 2(L%2)
-  sz[1] = __builtin_amdgcn_perm(X.vz, X.vs, 0x07060302u);   // (scale, zero) of group 2(L%2)+1
-  *reinterpret_cast<u32x2*>(slot + 2560 + 8 * lane) = sz;
-}
-
-// The V part of a staged tile in MFMA operand layout (read back from the LDS
-// slot; the K operands are read from the slot on demand):
-//   vc[i]  : V code bytes (2 x 8 bit) of tokens tau(g, 2i) (low 16 bits) and
-//            tau(g, 2i+1) (high 16 bits), channels 8m..8m+7
-//   vsz[j] : V scale (low half) and zero (high half) of token tau(g, j),
-//            channel group m/4
-struct QTileV {
-  uint32_t vc[4];
-  uint32_t vsz[8];
+// Accumulators of the KIVI tiles, kept beside WaveState (whose m and l they
+// share).  The PV product of a quantized tile is computed transposed,
+// O[head][channel] = P'[head][token] . codes[token][channel], with each MFMA
+// covering 16 channels of one 32-channel V quantization group, so the
+// per-token V scale folds into P' = p * scale and the zero point into a
+// per-(head, group) bias; the V codes enter the MFMA as they are.
+//   O[blk][r] : 2^-24 * sum_t P'[t][head 4g + r] * code[t][channel 16 blk + t]
+//               for lane (t, g) (codes enter as fp16 subnormals, see below)
+//   bv[grp]   : sum_t P'[t][head n] * zero[t][grp] over this lane's tokens
+struct QState {
+  float4v O[8];
+  float bv[4];
 };
 
-__device__ __forceinline__ void read_q_v(const char* slot, int lane, QTileV& X) {
+__device__ __forceinline__ void q_state_init(QState& qs) {
+#pragma unroll
+  for (int b = 0; b < 8; ++b) qs.O[b] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) qs.bv[i] = 0.f;
+}
+
+// Layout of a staged KIVI tile inside a wave slot (bytes):
+//   [0, 1024)     K codes, 8 byte rows x 128 channels (as stored)
+//   [1024, 1280)  K scales [128], [1280, 1536) K zeros [128]
+//   [1536, 2560)  V codes transposed: row b (0..31) holds code byte b of
+//                 tokens 0..31
+//   [2560, 2816)  V scales transposed [4 groups][32 tokens],
+//   [2816, 3072)  V zeros transposed
+constexpr int kQsK = 0, kQsKS = 1024, kQsKZ = 1280, kQsV = 1536, kQsVS = 2560, kQsVZ = 2816;
+
+__device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
+  *reinterpret_cast<u32x4*>(slot + kQsK + 16 * lane) = X.kc;
+  *reinterpret_cast<uint32_t*>(slot + kQsKS + 4 * lane) = X.ks;
+  *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = X.kz;
+  // lane L holds code bytes 16(L%2) .. +15 of token L/2
+  const int tok = lane >> 1, b0 = 16 * (lane & 1);
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    *reinterpret_cast<uint8_t*>(slot + kQsV + (b0 + i) * 32 + tok) =
+        (uint8_t)(X.vc[i >> 2] >> (8 * (i & 3)));
+  // lane L holds the scale / zero of token L/2, groups 2(L%2) and 2(L%2)+1
+  const int g0 = 2 * (lane & 1);
+  *reinterpret_cast<uint16_t*>(slot + kQsVS + g0 * 64 + 2 * tok) = (uint16_t)X.vs;
+  *reinterpret_cast<uint16_t*>(slot + kQsVS + (g0 + 1) * 64 + 2 * tok) = (uint16_t)(X.vs >> 16);
+  *reinterpret_cast<uint16_t*>(slot + kQsVZ + g0 * 64 + 2 * tok) = (uint16_t)X.vz;
+  *reinterpret_cast<uint16_t*>(slot + kQsVZ + (g0 + 1) * 64 + 2 * tok) = (uint16_t)(X.vz >> 16);
+}
+
+// Four 2-bit codes (one per byte of `w`, at bit `sh` of each byte) as four
+// fp16 values whose bit patterns are the codes themselves: the subnormals
+// code * 2^-24, which the fp16 MFMA multiplies without flushing (the 2^24 is
+// folded back into the logit scale and the final output).
+__device__ __forceinline__ u32x2 codes_as_f16(uint32_t w, uint32_t sh) {
+  const uint32_t c = (w >> sh) & 0x03030303u;
+  return u32x2{__builtin_amdgcn_perm(0u, c, 0x0c010c00u), __builtin_amdgcn_perm(0u, c, 0x0c030c02u)};
+}
+
+constexpr float kTwo24 = 16777216.0f;
+constexpr float kTwoM24 = 1.0f / 16777216.0f;
+
+// Consume one KIVI tile staged in the wave's LDS slot.
+//   QK: K is dequantized to fp16 as (code - zero) * scale.  fp16 patterns
+//       0x6400 | code are 1024 + code exactly; adding -(1024 + zero) gives
+//       code - zero exactly, and since min/max quantization keeps |code -
+//       zero| <= 2 except in rare groups, the product with the fp16 scale is
+//       the reference's value exactly.
+//   softmax: the reference max is refreshed whenever the tile's max exceeds
+//       it, so p <= 1 and P' = p * vscale stays within the fp16 range.
+// MIXED: the wave also holds fp16-tile accumulators in `st`, which a max
+// refresh rescales too.  Masked tokens get p = 0; their codes are finite.
+template <bool MIXED>
+__device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[4], int slot0,
+                                            int xlim, const SlotRanges& R, float scale_log2,
+                                            WaveState& st, QState& qs, int lane) {
   const int t = lane & 15, g = lane >> 4;
+  // scale and 1024 + zero of the lane's K channels 32c + 8g .. +7
+  half8 ks[4];
+  u32x4 kz1[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    ks[c] = *reinterpret_cast<const half8*>(slot + kQsKS + 2 * (32 * c + 8 * g));
+    kz1[c] = as_u4(*reinterpret_cast<const half8*>(slot + kQsKZ + 2 * (32 * c + 8 * g)) +
+                   (_Float16)1024.0f);
+  }
+
+  // S[token][head] on MFMA: lane (t, g) feeds token 16 blk + t, channels
+  // 32c + 8g .. +7 (code byte row (16 blk + t) / 4, bits 2 (t % 4))
+  const uint32_t sh = 2u * (uint32_t)(t & 3);
+  float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const u32x2 w =
+          *reinterpret_cast<const u32x2*>(slot + kQsK + (4 * blk + (t >> 2)) * 128 + 32 * c + 8 * g);
+      const uint32_t c0 = (w[0] >> sh) & 0x03030303u;
+      const uint32_t c1 = (w[1] >> sh) & 0x03030303u;
+      const u32x4 d = {pk_sub_f16(__builtin_amdgcn_perm(c0, 0x64646464u, 0x00050004u), kz1[c][0]),
+                       pk_sub_f16(__builtin_amdgcn_perm(c0, 0x64646464u, 0x00070006u), kz1[c][1]),
+                       pk_sub_f16(__builtin_amdgcn_perm(c1, 0x64646464u, 0x00050004u), kz1[c][2]),
+                       pk_sub_f16(__builtin_amdgcn_perm(c1, 0x64646464u, 0x00070006u), kz1[c][3])};
+      const u32x4 a = as_u4(as_h8(d) * ks[c]);
+      if (blk == 0)
+        s0 = mfma16x16x32(a, qB[c], s0);
+      else
+        s1 = mfma16x16x32(a, qB[c], s1);
+    }
+  }
+
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = (j < 4 ? s0[j & 3] : s1[j & 3]) * scale_log2;
+  if (!(xlim == kTile && tile_fully_valid(R, slot0))) {
+    const uint32_t valid = tile_valid_bits(R, slot0, xlim, lane);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = ((valid >> j) & 1u) ? x[j] : -INFINITY;
+  }
+  float lmax = x[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) lmax = fmaxf(lmax, x[j]);
+  if (__ballot(lmax > st.m)) {
+    float mt = fmaxf(lmax, __shfl_xor(lmax, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mnew = fmaxf(st.m, mt);
+    const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);   // head n (lane layout)
+    st.l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qs.bv[i] *= alpha;
+    if (MIXED) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) st.O[jj] = st.O[jj] * alpha;
+    }
+    // qs.O rows are heads 4g + r
+    float4v ar;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) qs.O[b] = qs.O[b] * ar;
+    st.m = mnew;
+  }
+  half8 pB;
+  float ls = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float p = __builtin_amdgcn_exp2f(x[j] - st.m);
+    ls += p;
+    pB[j] = (_Float16)p;
+  }
+  st.l += ls;
+
+  // P' per V group and the V zero-point bias; tokens tau(g, 0..3) = 4g..4g+3
+  // and tau(g, 4..7) = 16 + 4g .. +3 sit contiguously in the transposed rows.
+  half8 pq[4];
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const u32x2 s_lo = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 8 * g);
+    const u32x2 s_hi = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 32 + 8 * g);
+    const u32x2 z_lo = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 8 * g);
+    const u32x2 z_hi = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 32 + 8 * g);
+    const half8 vs = as_h8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
+    const half8 vz = as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]});
+    pq[grp] = pB * vs;
+    float b = qs.bv[grp];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      b = __builtin_amdgcn_fdot2(half2v{pq[grp][2 * i], pq[grp][2 * i + 1]},
+                                 half2v{vz[2 * i], vz[2 * i + 1]}, b, false);
+    qs.bv[grp] = b;
+  }
+
+  // O^T-free PV: lane (t, g) feeds the codes of channel 16 blk + t for the
+  // tokens tau(g, j) (transposed code byte row 4 blk + t/4, bits 2 (t % 4))
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk) {
+    const char* row = slot + kQsV + (4 * blk + (t >> 2)) * 32;
+    const uint32_t w0 = *reinterpret_cast<const uint32_t*>(row + 4 * g);
+    const uint32_t w1 = *reinterpret_cast<const uint32_t*>(row + 16 + 4 * g);
+    const u32x2 b0 = codes_as_f16(w0, sh), b1 = codes_as_f16(w1, sh);
+    const u32x4 b = {b0[0], b0[1], b1[0], b1[1]};
+    qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq[blk >> 1], as_h8(b), qs.O[blk], 0, 0, 0);
+  }
+}
+
+template <bool MIXED>
+__device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
+                                            const half8 (&qB)[4], int slot0, int xlim,
+                                            const SlotRanges& R, float scale_log2, WaveState& st,
+                                            QState& qs, int lane) {
+  stage_q_raw(raw, slot, lane);
+  q_tile_body<MIXED>(slot, qB, slot0, xlim, R, scale_log2, st, qs, lane);
+}
+
+// Row (head, channel) values of the quantized accumulators, ready for the
+// workgroup merge: O = 2^24 * qs.O - bias(head, group of channel).  The
+// per-head biases are reduced over the four lanes of a head and handed to
+// the lanes that hold the head's rows through the wave's scratch area
+// `tmp` (16 heads x 4 groups floats).
+__device__ __forceinline__ void q_state_rows(QState& qs, char* tmp, int lane) {
+  const int n = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = *reinterpret_cast<const uint16_t*>(slot + 1536 + tau(g, 2 * i) * 32 + 2 * t);
-    const uint32_t hi =
-        *reinterpret_cast<const uint16_t*>(slot + 1536 + tau(g, 2 * i + 1) * 32 + 2 * t);
-    X.vc[i] = lo | (hi << 16);
+    float b = qs.bv[i];
+    b += __shfl_xor(b, 16);
+    b += __shfl_xor(b, 32);
+    qs.bv[i] = b;
   }
+  if (g == 0) *reinterpret_cast<float4v*>(tmp + 16 * n) = float4v{qs.bv[0], qs.bv[1], qs.bv[2], qs.bv[3]};
+  float4v hb[4];   // bias of heads 4g + r, all four groups
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    X.vsz[j] = *reinterpret_cast<const uint32_t*>(slot + 2560 + tau(g, j) * 16 + 4 * (t >> 2));
-}
-
-// fp16 bit patterns 0x6400 | c encode 1024 + c exactly for c in 0..3; one
-// packed subtract of 1024 gives the code itself, a second subtract of the
-// stored fp16 zero gives c - z exactly while |c - z| <= 2048 (a rounding of
-// at most 2^-11 relative beyond), and the multiply by the fp16 scale is the
-// one rounding of the dequantized value (to fp16, the MFMA input type).
-
-// K operand of block blk, chunk c, read from the staged slot: the code bytes
-// of byte row (16*blk + t)/4 and the scales / zeros of channels 32c+8g..+7.
-__device__ __forceinline__ u32x4 decode_q_k(const char* slot, int blk, int c, int lane) {
-  const int t = lane & 15, g = lane >> 4;
-  const uint32_t sh = 2u * (uint32_t)(t & 3);   // token 16*blk + t sits at bits 2*(t%4)
-  const u32x2 kc =
-      *reinterpret_cast<const u32x2*>(slot + (4 * blk + (t >> 2)) * 128 + 32 * c + 8 * g);
-  const u32x4 ks = *reinterpret_cast<const u32x4*>(slot + 1024 + 2 * (32 * c + 8 * g));
-  const u32x4 kz = *reinterpret_cast<const u32x4*>(slot + 1280 + 2 * (32 * c + 8 * g));
-  const uint32_t c0 = (kc[0] >> sh) & 0x03030303u;
-  const uint32_t c1 = (kc[1] >> sh) & 0x03030303u;
-  u32x4 mg;
-  mg[0] = __builtin_amdgcn_perm(c0, 0x64646464u, 0x00050004u);
-  mg[1] = __builtin_amdgcn_perm(c0, 0x64646464u, 0x00070006u);
-  mg[2] = __builtin_amdgcn_perm(c1, 0x64646464u, 0x00050004u);
-  mg[3] = __builtin_amdgcn_perm(c1, 0x64646464u, 0x00070006u);
-  const half8 code = as_h8(mg) - (_Float16)1024.0f;
-  return as_u4((code - as_h8(kz)) * as_h8(ks));
-}
-
-// Dword w of V row j: channels 8m+2w and 8m+2w+1 sit at bits 4w and 4w+2 of
-// the row's 16 code bits; b | (b << 14) moves the second one to bit 16 + 4w.
-__device__ __forceinline__ uint32_t decode_q_v(const QTileV& X, int w, int j) {
-  const uint32_t b = (X.vc[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-  const uint32_t t0 = b | (b << 14);
-  const uint32_t mg = ((t0 >> (4 * w)) & 0x00030003u) | 0x64006400u;
-  // broadcast scale (low half) and zero (high half) to both halves
-  const half2v s2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(X.vsz[j], X.vsz[j], 0x01000100u));
-  const half2v z2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(X.vsz[j], X.vsz[j], 0x03020302u));
-  const half2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-  const half2v code = __builtin_bit_cast(half2v, mg) - k1024;
-  return __builtin_bit_cast(uint32_t, (code - z2) * s2);
-}
-
-// Consume one KIVI tile staged in the wave's LDS slot.  Masked tokens get
-// probability exactly 0 and their dequantized values are finite, so no row is
-// zeroed (the reference masks only its fp16 residual loads).
-__device__ __forceinline__ void q_tile_step(const char* slot, const half8 (&qB)[4], int slot0,
-                                            int xlim, const SlotRanges& R, float scale_log2,
-                                            WaveState& st, int lane) {
-  QTileV X;
-  read_q_v(slot, lane, X);
-  auto kop = [&](int blk, int c) { return decode_q_k(slot, blk, c, lane); };
-  auto vop = [&](int w, int j) { return decode_q_v(X, w, j); };
-  if (xlim == kTile && tile_fully_valid(R, slot0))
-    tile_body<true>(kop, vop, 0u, qB, scale_log2, st);
-  else
-    tile_body<false>(kop, vop, tile_valid_bits(R, slot0, xlim, lane), qB, scale_log2, st);
+  for (int r = 0; r < 4; ++r) hb[r] = *reinterpret_cast<const float4v*>(tmp + 16 * (4 * g + r));
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) qs.O[blk][r] = qs.O[blk][r] * kTwo24 - hb[r][blk >> 1];
 }
 
 }  // namespace kvdec

@@ -68,12 +68,17 @@ def test_split_plan_and_workspace_arithmetic():
     s = K.lib.kvdec_num_splits(K.KIND_DENSE, 1, 8, 163840)
     assert s > 1
     assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 1, 64, 8, 163840, 128) == 8 * s * 8 * 130 * 4
-    # every split keeps at least 2 tiles per wave of an 8-wave workgroup
+    # every split keeps at least one tile per wave of an 8-wave workgroup, and
+    # splits stop once the work units fill the 256 CUs
     for B in (1, 2, 4, 32):
         for L in (1, 2, 100, 8192, 32768, 131072, 163840):
             s = K.lib.kvdec_num_splits(K.KIND_DENSE, B, 8, L)
             tiles = -(-L // 32)
-            assert s == 1 or tiles / s >= 16, (B, L, s)
+            assert s == 1 or tiles / s >= 8, (B, L, s)
+            assert s == 1 or B * 8 * (s - 1) < 256, (B, L, s)
+    # the fused KIVI decode never splits (one work unit per KV head)
+    assert K.lib.kvdec_num_splits(K.KIND_KIVI, 1, 8, 4096) == 1
+    assert K.lib.kvdec_workspace_bytes(K.KIND_KIVI, 1, 64, 8, 4096, 128) == 0
     # invalid heads -> no workspace
     assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 32, 64, 7, 1000, 128) == 0
     assert K.lib.kvdec_workspace_bytes(K.KIND_DENSE, 32, 64, 8, 1000, 64) == 0
@@ -149,7 +154,6 @@ def test_kivi_validation():
     assert _kivi(W=128 + 48) == E["GROUP"]                            # window-old not whole groups
     assert _kivi(seq_len=0) == E["SEQLEN"]
     assert _kivi(KVH=3) == E["SHAPE"]
-    assert _kivi(B=1, W=8192) == E["WORKSPACE"]
 
 
 def _quant(fn, **kw):
