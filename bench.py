@@ -1,26 +1,34 @@
 """Decode-attention benchmark on one MI355X: prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--paths kivi,dense,sparse,quantize]
-                    [--no-cpu] [--flush-mib 1024]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--paths kivi,dense,sparse,quantize,sweep]
+                    [--no-cpu] [--no-latency]
 
 Workload (the BASELINE metric's configuration): B=32, 64 query / 8 KV heads,
 head_dim 128, logical context L=163840, sink S=4, window W=256, KIVI residual
 R=128, fp16 inputs ~ N(0,1) from a fixed seed with 4 of the 128 K channels
-scaled x10.  A "step" is one decode call of a path over the whole batch with
-its inputs resident in HBM:
+scaled x10.  A "step" is one decode call of a path over the whole batch:
 
   kivi      fused sink+window(W=256)+KIVI-2bit decode (the headline ``value``)
-  dense     dense GQA decode over all 163840 tokens
-  sparse    fp16 sink+window(W=256) decode
-  quantize  KIVI quantization of the [32, 8, 163840, 128] K cache (config 4)
+  dense     dense GQA decode over all 163840 tokens (and L=32768, config 2)
+  sparse    fp16 sink+window(W=256) decode (config 3)
+  quantize  KIVI quantization of the [32, 8, 163840, 128] K and V caches (config 4)
+  sweep     the fused decode at W = 1024 and 4096 (config 5; W=32 < R is
+            outside the reference's domain)
 
-Each timed step is bracketed by its own HIP events on torch's current stream
-(the stream the kernels are launched on) and preceded by a write of a
-1 GiB buffer, which evicts L2 and the 256 MB Infinity Cache, so every step
-starts cold.  ``ms_per_step`` is the mean per-step event time; ``warm_us`` is
-the back-to-back time per step without flushes.  The CPU baseline times the
-numpy oracle (the repository's own restatement of the reference's PyTorch
-formulas) on the host on a bounded sample of the same workload.
+Timing.  Each path keeps several independent input sets resident in HBM
+(together >= 1 GiB, more than L2 plus the 256 MB Infinity Cache) and captures
+K back-to-back calls that cycle through them in one HIP graph; the graph is
+replayed W times untimed, then once between two HIP events on the capture
+stream.  ``ms_per_step`` / ``value`` = that time / K: the steady-state cost
+of a decode step whose inputs are cold in every cache, with launches
+pipelined as in a decode loop.  ``latency_us`` is the reference harness's
+method (triton do_bench): a 1 GiB buffer write before each single call,
+events around the call; it adds the per-call dispatch latency (about 5 us
+on this system for an empty kernel).
+
+The CPU baseline times the numpy oracle (the repository's own restatement of
+the reference's PyTorch formulas) on the host on a bounded sample of the same
+workload.
 """
 
 from __future__ import annotations
@@ -46,6 +54,8 @@ S, W, R = 4, 256, 128
 HBM_PEAK_GBS = 8000.0
 REF_KIVI_W256_US = 240.87          # A100 Triton, results/benchmark_results_quantized.csv:43
 METRIC = "decode-attn µs/step + achieved HBM TB/s (% of peak), B=32 L=163840 W=256"
+COLD_SET_BYTES = 1 << 30           # rotating input sets per path: at least this many bytes
+MAX_SETS = 64
 
 
 # --------------------------------------------------------------------------
@@ -79,8 +89,8 @@ def bytes_kivi(window, residual=R, sink_tokens=S):
     return bytes_q_o() + pairs * (2 * residual * D * 2 + k_codes + k_meta + v_codes + v_meta)
 
 
-def bytes_quantize_k(n_tok):
-    """Read fp16 K, write codes and fp16 scale/zero."""
+def bytes_quantize(n_tok):
+    """Read fp16 input, write codes and fp16 scale/zero (the same for K and V)."""
     pairs = B * KVH
     return pairs * (n_tok * D * 2 + n_tok * D // 4 + 2 * 2 * (n_tok // 32) * D)
 
@@ -89,47 +99,79 @@ def bytes_quantize_k(n_tok):
 # timing
 # --------------------------------------------------------------------------
 
-def time_steps(fn, steps, warmup, flush):
-    """Per-step HIP-event times (ms) with a cache flush before each step, plus
-    the back-to-back (warm) time per step."""
-    for _ in range(warmup):
-        fn()
+def graph_time(call, nsets, steps, warmup):
+    """Per-step ms of `steps` back-to-back calls call(i % nsets), captured in
+    one HIP graph and replayed; returns (ms_per_step, outputs of the capture)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(min(3, steps)):
+            call(i % nsets)
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
+    g = torch.cuda.CUDAGraph()
+    outs = []
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            outs.append(call(i % nsets))
+    for _ in range(max(1, warmup)):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, outs
+
+
+def latency_time(call, nsets, reps, flush):
+    """Reference-harness latency: 1 GiB write, then events around one call."""
+    for i in range(3):
+        call(i % nsets)
+    torch.cuda.synchronize()
+    per = []
+    for i in range(reps):
         flush.zero_()
-        starts[i].record()
-        fn()
-        ends[i].record()
-    torch.cuda.synchronize()
-    region_s = time.perf_counter() - t0
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    w0 = torch.cuda.Event(enable_timing=True)
-    w1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    w0.record()
-    for _ in range(steps):
-        fn()
-    w1.record()
-    torch.cuda.synchronize()
-    warm_ms = w0.elapsed_time(w1) / steps
-    return {"mean_ms": float(np.mean(per)), "median_ms": float(np.median(per)),
-            "min_ms": float(np.min(per)), "warm_ms": warm_ms, "region_s": region_s}
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        call(i % nsets)
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1))
+    return float(np.mean(per)), float(np.median(per))
 
 
-def path_record(t, alg_bytes, alg_bytes_ref=None):
-    us = t["mean_ms"] * 1e3
-    gbs = alg_bytes / (t["mean_ms"] * 1e-3) / 1e9
-    rec = {"us_per_step": round(us, 3), "median_us": round(t["median_ms"] * 1e3, 3),
-           "min_us": round(t["min_ms"] * 1e3, 3), "warm_us": round(t["warm_ms"] * 1e3, 3),
+def path_record(ms, alg_bytes, nsets, steps, alg_bytes_ref=None, latency=None):
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    rec = {"us_per_step": round(ms * 1e3, 3), "steps": steps, "input_sets": nsets,
            "alg_bytes": int(alg_bytes), "achieved_GBs": round(gbs, 1),
            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
     if alg_bytes_ref is not None:
         rec["alg_bytes_ref_accounting"] = int(alg_bytes_ref)
-        rec["achieved_GBs_ref_accounting"] = round(alg_bytes_ref / (t["mean_ms"] * 1e-3) / 1e9, 1)
+        rec["achieved_GBs_ref_accounting"] = round(alg_bytes_ref / (ms * 1e-3) / 1e9, 1)
+    if latency is not None:
+        rec["latency_us"] = round(latency[0] * 1e3, 3)
+        rec["latency_median_us"] = round(latency[1] * 1e3, 3)
     return rec
+
+
+def measured_traffic(key):
+    """HBM bytes per launch of the path's kernel, as recorded from the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs in profiles/hbm_traffic.json
+    (calibrated against a 256 MiB copy); None when not recorded."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            rec = json.load(f).get(key)
+        return None if rec is None else int(rec["fetch_bytes_per_launch"] + rec["write_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def n_sets(bytes_per_set):
+    return int(max(1, min(MAX_SETS, -(-COLD_SET_BYTES // bytes_per_set))))
 
 
 # --------------------------------------------------------------------------
@@ -178,14 +220,24 @@ def cpu_baseline_dense(q, k, v, rows=1):
 
 # --------------------------------------------------------------------------
 
+KIVI_KEYS = ("k_residual", "v_residual",
+             "k_sink_packed", "k_sink_scale", "k_sink_zero",
+             "v_sink_packed", "v_sink_scale", "v_sink_zero",
+             "k_win_packed", "k_win_scale", "k_win_zero",
+             "v_win_packed", "v_win_scale", "v_win_zero")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--paths", default="kivi,dense,sparse,quantize")
+    ap.add_argument("--paths", default="kivi,dense,sparse,quantize,sweep")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--flush-mib", type=int, default=1024)
+    ap.add_argument("--no-latency", action="store_true", help="skip the per-call latency runs")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first copy 256 MiB device-to-device three times: the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -198,64 +250,113 @@ def main():
     import sparse_kernel
 
     paths = [p.strip() for p in args.paths.split(",") if p.strip()]
+    K, Wu = max(1, args.steps), max(1, args.warmup)
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(0)
     outliers = torch.randperm(D, generator=torch.Generator().manual_seed(0))[:4].tolist()
-    flush = torch.empty(args.flush_mib * (1 << 20) // 4, dtype=torch.int32, device=dev)
+    flush = None if args.no_latency else torch.empty((1 << 30) // 4, dtype=torch.int32, device=dev)
 
     def randn(*shape):
         return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float16)
 
-    q = randn(B, H, D)
+    def compacted(window):
+        kc = randn(B, KVH, S + window, D)
+        kc[..., outliers] *= 10
+        return kc, randn(B, KVH, S + window, D)
+
     out = {}
     cpu = None
 
-    if "kivi" in paths or "sparse" in paths:
-        kc = randn(B, KVH, S + W, D)
-        kc[..., outliers] *= 10
-        vc = randn(B, KVH, S + W, D)
-        if "sparse" in paths:
-            t = time_steps(lambda: sparse_kernel.sparse_decode_attention(q, kc, vc, seq_len=L, window=W),
-                           args.steps, args.warmup, flush)
-            out["sparse_fp16_w256"] = path_record(t, bytes_sparse(W))
-        if "kivi" in paths:
-            cache = quant_kernel.build_quantized_kv_cache(kc, vc)
-            args_kivi = [cache[k] for k in (
-                "k_residual", "v_residual",
-                "k_sink_packed", "k_sink_scale", "k_sink_zero",
-                "v_sink_packed", "v_sink_scale", "v_sink_zero",
-                "k_win_packed", "k_win_scale", "k_win_zero",
-                "v_win_packed", "v_win_scale", "v_win_zero")]
-            t = time_steps(lambda: quant_kernel.sparse_decode_attention_quantized(
-                q, *args_kivi, seq_len=L, window=W), args.steps, args.warmup, flush)
-            out["kivi_w256"] = path_record(t, bytes_kivi(W), bytes_kivi(W, sink_tokens=32))
-            if not args.no_cpu:
-                us, reps = cpu_baseline_kivi(q, cache)
-                cpu = {"value": round(us, 1), "unit": "us/step", "cores": _blas_threads(),
-                       "kind": "port",
-                       "sample": f"the full kivi_w256 step (B=32, all 256 KV heads), numpy oracle "
-                                 f"dequantize-then-attend in float32, median of {reps} reps"}
+    if args.copy_calibration:
+        src = torch.ones((256 << 20) // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
-    if "dense" in paths or "quantize" in paths:
+    def kivi_path(window, steps, name, with_cpu=False):
+        nonlocal cpu
+        ns = n_sets(bytes_kivi(window))
+        sets = []
+        for _ in range(ns):
+            kc, vc = compacted(window)
+            cache = quant_kernel.build_quantized_kv_cache(kc, vc)
+            del kc, vc
+            sets.append((randn(B, H, D), [cache[k] for k in KIVI_KEYS], cache))
+
+        def call(i):
+            q, a, _ = sets[i]
+            return quant_kernel.sparse_decode_attention_quantized(q, *a, seq_len=L, window=window)
+
+        ms, _ = graph_time(call, ns, steps, Wu)
+        lat = None if flush is None else latency_time(call, ns, 50, flush)
+        out[name] = path_record(ms, bytes_kivi(window), ns, steps, bytes_kivi(window, sink_tokens=32), lat)
+        if with_cpu and not args.no_cpu:
+            us, reps = cpu_baseline_kivi(sets[0][0], sets[0][2])
+            cpu = {"value": round(us, 1), "unit": "us/step", "cores": _blas_threads(), "kind": "port",
+                   "sample": f"the full kivi_w256 step (B=32, all 256 KV heads), numpy oracle "
+                             f"dequantize-then-attend in float32, median of {reps} reps"}
+        del sets
+
+    if "kivi" in paths:
+        kivi_path(W, K, "kivi_w256", with_cpu=True)
+
+    if "sweep" in paths:
+        for w in (1024, 4096):
+            kivi_path(w, K, f"kivi_w{w}")
+
+    if "sparse" in paths:
+        ns = n_sets(bytes_sparse(W))
+        sets = [(randn(B, H, D),) + compacted(W) for _ in range(ns)]
+
+        def call(i):
+            q, kc, vc = sets[i]
+            return sparse_kernel.sparse_decode_attention(q, kc, vc, seq_len=L, window=W)
+
+        ms, _ = graph_time(call, ns, K, Wu)
+        lat = None if flush is None else latency_time(call, ns, 50, flush)
+        out["sparse_fp16_w256"] = path_record(ms, bytes_sparse(W), ns, K, latency=lat)
+        del sets
+
+    if "quantize" in paths or "dense" in paths:
         k = randn(B, KVH, L, D)
         k[..., outliers] *= 10
+        v = randn(B, KVH, L, D)
+        q = randn(B, H, D)
         if "quantize" in paths:
-            t = time_steps(lambda: quant_kernel.quantize_k_cache(k), max(3, args.steps // 10),
-                           max(1, args.warmup // 5), flush)
-            out["quantize_k_L163840"] = path_record(t, bytes_quantize_k(L))
+            qsteps = max(3, K // 10)
+            ms, _ = graph_time(lambda i: quant_kernel.quantize_k_cache(k), 1, qsteps, 1)
+            out["quantize_k_L163840"] = path_record(ms, bytes_quantize(L), 1, qsteps)
+            ms, _ = graph_time(lambda i: quant_kernel.quantize_v_cache(v), 1, qsteps, 1)
+            out["quantize_v_L163840"] = path_record(ms, bytes_quantize(L), 1, qsteps)
         if "dense" in paths:
-            v = randn(B, KVH, L, D)
-            t = time_steps(lambda: dense_kernel.dense_decode_attention(q, k, v, seq_len=L),
-                           max(3, args.steps // 5), max(1, args.warmup // 5), flush)
-            out["dense_L163840"] = path_record(t, bytes_dense(L))
+            dsteps = max(3, K // 5)
+            ms, _ = graph_time(lambda i: dense_kernel.dense_decode_attention(q, k, v, seq_len=L), 1,
+                               dsteps, 1)
+            out["dense_L163840"] = path_record(ms, bytes_dense(L), 1, dsteps)
             if not args.no_cpu:
                 us, reps = cpu_baseline_dense(q, k, v)
                 out["dense_L163840"]["cpu_baseline"] = {
                     "value": round(us, 1), "unit": "us/step", "cores": _blas_threads(), "kind": "port",
                     "sample": f"batch row 0 of 32 at L=163840 (numpy oracle, float32, median of "
                               f"{reps} reps), scaled x32"}
-            del v
-        del k
+            # config 2: L = 32768 (a prefix view of the same cache would not be
+            # contiguous, so the cache is regenerated at that length)
+            del k, v
+            Ls = 32768
+            ns = n_sets(bytes_dense(Ls))
+            dsets = [(randn(B, H, D), randn(B, KVH, Ls, D), randn(B, KVH, Ls, D)) for _ in range(ns)]
+
+            def dcall(i):
+                qq, kk, vv = dsets[i]
+                return dense_kernel.dense_decode_attention(qq, kk, vv, seq_len=Ls)
+
+            ms, _ = graph_time(dcall, ns, max(3, K // 2), 1)
+            out["dense_L32768"] = path_record(ms, bytes_dense(Ls), ns, max(3, K // 2))
+            del dsets
+        else:
+            del k, v
 
     head_key = "kivi_w256" if "kivi_w256" in out else next(iter(out))
     head = out[head_key]
@@ -265,8 +366,8 @@ def main():
         "value": value,
         "unit": "us/step",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": K,
+        "warmup": Wu,
         "ms_per_step": round(value / 1e3, 6),
         "higher_is_better": False,
         "scaling": "weak",
@@ -275,9 +376,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{head_key}: B=32 H=64 KVH=8 D=128 L=163840 S=4 W=256 R=128, "
                                "fp16 N(0,1), 4 K channels x10",
-                   "flush_mib_per_step": args.flush_mib},
+                   "timing": "HIP-graph replay of back-to-back steps over rotating cold input sets"},
         "roofline": {"bound": "hbm", "achieved": head["achieved_GBs"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": head["frac_of_peak"], "traffic": None},
+                     "unit": "GB/s", "frac": head["frac_of_peak"], "traffic": measured_traffic(head_key)},
         "cpu_baseline": cpu,
         "paths": out,
     }

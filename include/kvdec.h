@@ -139,6 +139,9 @@ int kvdec_quantize_v(const void* x, int in_dtype, void* packed_u8,
  *   window-old token s - sink, or residual row s - (sink + window - residual);
  *   slots are masked by _kv_indices validity.  window >= residual,
  *   (window - residual) % group == 0, residual % 32 == 0, sink <= group.
+ *   Runs in one pass (one workgroup per KV head): ws / ws_bytes are
+ *   accepted for interface stability and ignored (kvdec_workspace_bytes
+ *   returns 0 for KVDEC_KIND_KIVI).
  */
 int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res,
                              const void* const* kivi, void* o, int64_t B,

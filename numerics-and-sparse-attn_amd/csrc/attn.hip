@@ -47,14 +47,12 @@ struct AttnCommon {
 };
 
 // LDS of a workgroup (bytes): two work counters, the per-wave max / sum of
-// 16 heads, a 256-byte scratch area per wave, then one 8 KB slot per wave
-// (K tile staging, KIVI tile staging, and at the end that wave's partial
-// output rows).
+// 16 heads, then one 8 KB slot per wave (K tile staging, KIVI tile staging,
+// and at the end that wave's partial output rows).
 constexpr int kLdsCtr = 0;
 constexpr int kLdsM = 16;
 constexpr int kLdsL = kLdsM + kWaves * kMaxGroup * 4;
-constexpr int kLdsTmp = kLdsL + kWaves * kMaxGroup * 4;
-constexpr int kLdsSlots = (kLdsTmp + kWaves * 256 + 255) & ~255;
+constexpr int kLdsSlots = (kLdsL + kWaves * kMaxGroup * 4 + 255) & ~255;
 constexpr int kLdsBytes = kLdsSlots + kWaves * kSlotBytes;
 static_assert(kMaxGroup * kHeadDim * 4 <= kSlotBytes, "partial output must fit a wave slot");
 
@@ -204,19 +202,33 @@ __device__ __forceinline__ void publish_f(const AttnCommon& P, const WaveState& 
 }
 
 // Quantized-tile accumulators: lane (t, g) holds head 4g + r, channel
-// 16 blk + t.  ADD: the slot already holds this wave's fp16-tile rows.
+// 16 blk + t.  All 16 head rows are written (rows of heads >= G stay inside
+// the wave's slot and the merge never reads them), so no write is
+// predicated.  ADD: the slot already holds this wave's fp16-tile rows (all
+// reads are issued before any write, so the adds wait on LDS once).
 template <bool ADD>
-__device__ __forceinline__ void publish_q(QState& qs, char* slot, char* tmp, int lane) {
-  q_state_rows(qs, tmp, lane);
+__device__ __forceinline__ void publish_q(QState& qs, char* slot, int lane) {
   const int t = lane & 15, g = lane >> 4;
+  uint32_t off[8][4];
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int h = 4 * g + r;
-      float* p = reinterpret_cast<float*>(slot + row_off(h, 4 * blk + (t >> 2)) + 4 * (t & 3));
-      *p = ADD ? *p + qs.O[blk][r] : qs.O[blk][r];
-    }
+    for (int r = 0; r < 4; ++r) off[blk][r] = row_off(4 * g + r, 4 * blk + (t >> 2)) + 4 * (t & 3);
+  if (ADD) {
+    float prev[8][4];
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) prev[blk][r] = *reinterpret_cast<const float*>(slot + off[blk][r]);
+#pragma unroll
+    for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) qs.O[blk][r] += prev[blk][r];
+  }
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) *reinterpret_cast<float*>(slot + off[blk][r]) = qs.O[blk][r];
 }
 
 // Barrier, then combine the waves' published partials into the output (one
@@ -228,35 +240,42 @@ __device__ __forceinline__ void merge_out(const AttnCommon& P, char* lds, int64_
   const int64_t b = pair / P.KVH;
   const int kvh = (int)(pair % P.KVH);
   const size_t total = (size_t)P.pairs * P.n_splits * P.G;
-  // One thread per (head, 4-channel chunk).
-  for (int e = threadIdx.x; e < P.G * 32; e += kThreads) {
-    const int hn = e >> 5, ch = e & 31;
-    float M = kMaxSentinel;
+  // One thread per (head, 4-channel chunk): G * 32 <= 512 = kThreads.  All
+  // LDS reads are issued before the first use.
+  const int e = threadIdx.x;
+  if (e >= P.G * 32) return;
+  const int hn = e >> 5, ch = e & 31;
+  float mw[kWaves], lw[kWaves];
+  float4v ow[kWaves];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sh_m[w * kMaxGroup + hn]);
-    float L = 0.f;
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
+  for (int w = 0; w < kWaves; ++w) {
+    mw[w] = sh_m[w * kMaxGroup + hn];
+    lw[w] = sh_l[w * kMaxGroup + hn];
+    ow[w] = *reinterpret_cast<const float4v*>(lds + kLdsSlots + w * kSlotBytes + row_off(hn, ch));
+  }
+  float M = mw[0];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = __builtin_amdgcn_exp2f(sh_m[w * kMaxGroup + hn] - M);
-      L += sh_l[w * kMaxGroup + hn] * f;
-      const float4v o =
-          *reinterpret_cast<const float4v*>(lds + kLdsSlots + w * kSlotBytes + row_off(hn, ch));
-      acc += o * f;
-    }
-    if (P.n_splits == 1) {
-      const float inv = 1.0f / L;
-      half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
-                  (_Float16)(acc[3] * inv)};
-      *reinterpret_cast<half4v*>(P.o + ((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim +
-                                 4 * ch) = h;
-    } else {
-      const size_t idx = ((size_t)pair * P.n_splits + split) * P.G + hn;
-      *reinterpret_cast<float4v*>(P.ws + idx * kHeadDim + 4 * ch) = acc;
-      if (ch == 0) {
-        P.ws[total * kHeadDim + idx] = M;
-        P.ws[total * kHeadDim + total + idx] = L;
-      }
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, mw[w]);
+  float L = 0.f;
+  float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float f = __builtin_amdgcn_exp2f(mw[w] - M);
+    L += lw[w] * f;
+    acc += ow[w] * f;
+  }
+  if (P.n_splits == 1) {
+    const float inv = 1.0f / L;
+    half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
+                (_Float16)(acc[3] * inv)};
+    *reinterpret_cast<half4v*>(P.o + ((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim +
+                               4 * ch) = h;
+  } else {
+    const size_t idx = ((size_t)pair * P.n_splits + split) * P.G + hn;
+    *reinterpret_cast<float4v*>(P.ws + idx * kHeadDim + 4 * ch) = acc;
+    if (ch == 0) {
+      P.ws[total * kHeadDim + idx] = M;
+      P.ws[total * kHeadDim + total + idx] = L;
     }
   }
 }
@@ -415,7 +434,7 @@ struct KiviSrc {
       }
       publish_ml(P, st, c.lds, lane, wave);
       publish_f(P, st, c.slot, lane);
-      if (has_q) publish_q<true>(qs, c.slot, c.lds + kLdsTmp + wave * 256, lane);
+      if (has_q) publish_q<true>(qs, c.slot, lane);
     } else {
       Ring<QItems<false>> qring;
       ring_begin(qonly, qring, qw, qw + nqw + nrw, lane);
@@ -425,7 +444,7 @@ struct KiviSrc {
       else
         ring_run_static(qonly, qring, qref, c);
       publish_ml(P, st, c.lds, lane, wave);
-      publish_q<false>(qs, c.slot, c.lds + kLdsTmp + wave * 256, lane);
+      publish_q<false>(qs, c.slot, lane);
     }
   }
 };

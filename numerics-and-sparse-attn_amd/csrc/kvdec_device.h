@@ -300,23 +300,19 @@ __device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, bool valid,
 
 // Accumulators of the KIVI tiles, kept beside WaveState (whose m and l they
 // share).  The PV product of a quantized tile is computed transposed,
-// O[head][channel] = P'[head][token] . codes[token][channel], with each MFMA
-// covering 16 channels of one 32-channel V quantization group, so the
-// per-token V scale folds into P' = p * scale and the zero point into a
-// per-(head, group) bias; the V codes enter the MFMA as they are.
-//   O[blk][r] : 2^-24 * sum_t P'[t][head 4g + r] * code[t][channel 16 blk + t]
-//               for lane (t, g) (codes enter as fp16 subnormals, see below)
-//   bv[grp]   : sum_t P'[t][head n] * zero[t][grp] over this lane's tokens
+// O[head][channel] = P'[head][token] . (code - zero)[token][channel], with
+// each MFMA covering 16 channels of one 32-channel V quantization group, so
+// the per-token V scale folds into P' = p * scale and the B operand is the
+// exact small integer code - zero.
+//   O[blk][r] : sum_t P'[t][head 4g + r] * (code - zero)[t][channel 16 blk + t]
+//               for lane (t, g)
 struct QState {
   float4v O[8];
-  float bv[4];
 };
 
 __device__ __forceinline__ void q_state_init(QState& qs) {
 #pragma unroll
   for (int b = 0; b < 8; ++b) qs.O[b] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) qs.bv[i] = 0.f;
 }
 
 // Layout of a staged KIVI tile inside a wave slot (bytes):
@@ -346,17 +342,12 @@ __device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int l
   *reinterpret_cast<uint16_t*>(slot + kQsVZ + (g0 + 1) * 64 + 2 * tok) = (uint16_t)(X.vz >> 16);
 }
 
-// Four 2-bit codes (one per byte of `w`, at bit `sh` of each byte) as four
-// fp16 values whose bit patterns are the codes themselves: the subnormals
-// code * 2^-24, which the fp16 MFMA multiplies without flushing (the 2^24 is
-// folded back into the logit scale and the final output).
-__device__ __forceinline__ u32x2 codes_as_f16(uint32_t w, uint32_t sh) {
-  const uint32_t c = (w >> sh) & 0x03030303u;
-  return u32x2{__builtin_amdgcn_perm(0u, c, 0x0c010c00u), __builtin_amdgcn_perm(0u, c, 0x0c030c02u)};
+// Two codes of `c` (one code per byte; sel 0x00050004 takes bytes 0 and 1,
+// 0x00070006 bytes 2 and 3) as the fp16 pair (1024 + code_a, 1024 + code_b):
+// the patterns 0x6400 | code.
+__device__ __forceinline__ uint32_t codes_1024(uint32_t c, uint32_t sel) {
+  return __builtin_amdgcn_perm(c, 0x64646464u, sel);
 }
-
-constexpr float kTwo24 = 16777216.0f;
-constexpr float kTwoM24 = 1.0f / 16777216.0f;
 
 // Consume one KIVI tile staged in the wave's LDS slot.
 //   QK: K is dequantized to fp16 as (code - zero) * scale.  fp16 patterns
@@ -395,10 +386,10 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
           *reinterpret_cast<const u32x2*>(slot + kQsK + (4 * blk + (t >> 2)) * 128 + 32 * c + 8 * g);
       const uint32_t c0 = (w[0] >> sh) & 0x03030303u;
       const uint32_t c1 = (w[1] >> sh) & 0x03030303u;
-      const u32x4 d = {pk_sub_f16(__builtin_amdgcn_perm(c0, 0x64646464u, 0x00050004u), kz1[c][0]),
-                       pk_sub_f16(__builtin_amdgcn_perm(c0, 0x64646464u, 0x00070006u), kz1[c][1]),
-                       pk_sub_f16(__builtin_amdgcn_perm(c1, 0x64646464u, 0x00050004u), kz1[c][2]),
-                       pk_sub_f16(__builtin_amdgcn_perm(c1, 0x64646464u, 0x00070006u), kz1[c][3])};
+      const u32x4 d = {pk_sub_f16(codes_1024(c0, 0x00050004u), kz1[c][0]),
+                       pk_sub_f16(codes_1024(c0, 0x00070006u), kz1[c][1]),
+                       pk_sub_f16(codes_1024(c1, 0x00050004u), kz1[c][2]),
+                       pk_sub_f16(codes_1024(c1, 0x00070006u), kz1[c][3])};
       const u32x4 a = as_u4(as_h8(d) * ks[c]);
       if (blk == 0)
         s0 = mfma16x16x32(a, qB[c], s0);
@@ -424,8 +415,6 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
     const float mnew = fmaxf(st.m, mt);
     const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);   // head n (lane layout)
     st.l *= alpha;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qs.bv[i] *= alpha;
     if (MIXED) {
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) st.O[jj] = st.O[jj] * alpha;
@@ -448,35 +437,34 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   }
   st.l += ls;
 
-  // P' per V group and the V zero-point bias; tokens tau(g, 0..3) = 4g..4g+3
-  // and tau(g, 4..7) = 16 + 4g .. +3 sit contiguously in the transposed rows.
+  // P' per V group and 1024 + zero of the lane's tokens: tokens
+  // tau(g, 0..3) = 4g..4g+3 and tau(g, 4..7) = 16 + 4g .. +3 sit
+  // contiguously in the transposed rows.
   half8 pq[4];
+  u32x4 vz1[4];
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
     const u32x2 s_lo = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 8 * g);
     const u32x2 s_hi = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 32 + 8 * g);
     const u32x2 z_lo = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 8 * g);
     const u32x2 z_hi = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 32 + 8 * g);
-    const half8 vs = as_h8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
-    const half8 vz = as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]});
-    pq[grp] = pB * vs;
-    float b = qs.bv[grp];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      b = __builtin_amdgcn_fdot2(half2v{pq[grp][2 * i], pq[grp][2 * i + 1]},
-                                 half2v{vz[2 * i], vz[2 * i + 1]}, b, false);
-    qs.bv[grp] = b;
+    pq[grp] = pB * as_h8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
+    vz1[grp] = as_u4(as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]}) + (_Float16)1024.0f);
   }
 
-  // O^T-free PV: lane (t, g) feeds the codes of channel 16 blk + t for the
-  // tokens tau(g, j) (transposed code byte row 4 blk + t/4, bits 2 (t % 4))
+  // PV: lane (t, g) feeds code - zero of channel 16 blk + t for the tokens
+  // tau(g, j) (transposed code byte row 4 blk + t/4, bits 2 (t % 4)); the
+  // subtraction of 1024 + zero from 1024 + code is exact.
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     const char* row = slot + kQsV + (4 * blk + (t >> 2)) * 32;
-    const uint32_t w0 = *reinterpret_cast<const uint32_t*>(row + 4 * g);
-    const uint32_t w1 = *reinterpret_cast<const uint32_t*>(row + 16 + 4 * g);
-    const u32x2 b0 = codes_as_f16(w0, sh), b1 = codes_as_f16(w1, sh);
-    const u32x4 b = {b0[0], b0[1], b1[0], b1[1]};
+    const uint32_t c0 = (*reinterpret_cast<const uint32_t*>(row + 4 * g) >> sh) & 0x03030303u;
+    const uint32_t c1 = (*reinterpret_cast<const uint32_t*>(row + 16 + 4 * g) >> sh) & 0x03030303u;
+    const u32x4 z = vz1[blk >> 1];
+    const u32x4 b = {pk_sub_f16(codes_1024(c0, 0x00050004u), z[0]),
+                     pk_sub_f16(codes_1024(c0, 0x00070006u), z[1]),
+                     pk_sub_f16(codes_1024(c1, 0x00050004u), z[2]),
+                     pk_sub_f16(codes_1024(c1, 0x00070006u), z[3])};
     qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq[blk >> 1], as_h8(b), qs.O[blk], 0, 0, 0);
   }
 }
@@ -488,30 +476,6 @@ __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
                                             QState& qs, int lane) {
   stage_q_raw(raw, slot, lane);
   q_tile_body<MIXED>(slot, qB, slot0, xlim, R, scale_log2, st, qs, lane);
-}
-
-// Row (head, channel) values of the quantized accumulators, ready for the
-// workgroup merge: O = 2^24 * qs.O - bias(head, group of channel).  The
-// per-head biases are reduced over the four lanes of a head and handed to
-// the lanes that hold the head's rows through the wave's scratch area
-// `tmp` (16 heads x 4 groups floats).
-__device__ __forceinline__ void q_state_rows(QState& qs, char* tmp, int lane) {
-  const int n = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float b = qs.bv[i];
-    b += __shfl_xor(b, 16);
-    b += __shfl_xor(b, 32);
-    qs.bv[i] = b;
-  }
-  if (g == 0) *reinterpret_cast<float4v*>(tmp + 16 * n) = float4v{qs.bv[0], qs.bv[1], qs.bv[2], qs.bv[3]};
-  float4v hb[4];   // bias of heads 4g + r, all four groups
-#pragma unroll
-  for (int r = 0; r < 4; ++r) hb[r] = *reinterpret_cast<const float4v*>(tmp + 16 * (4 * g + r));
-#pragma unroll
-  for (int blk = 0; blk < 8; ++blk)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) qs.O[blk][r] = qs.O[blk][r] * kTwo24 - hb[r][blk >> 1];
 }
 
 }  // namespace kvdec
