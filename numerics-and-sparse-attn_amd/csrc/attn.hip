@@ -14,8 +14,8 @@
 // benchmark shapes (B*KVH = 256 KV heads) every path runs in one pass.
 //
 // KIVI units have two queues: the fp16 residual tiles go to the first waves
-// (one each while there are enough waves), the quantized tiles (sink group
-// first, then the window-old groups) to the others; a wave that finishes its
+// (one each while there are enough waves), the quantized tiles (window-old
+// groups, then the sink group) to the others; a wave that finishes its
 // residual tiles joins the quantized queue.
 
 #include "kvdec_device.h"
@@ -94,17 +94,18 @@ struct QRef {
   QState& qs;
 };
 
-// Quantized tiles of one KV head: item 0 is the sink group (`sink` real
-// tokens at slots 0..sink-1), item i > 0 is window-old group i-1 (slots
-// sink + 32(i-1) ..).  MIXED: the wave also holds fp16-tile accumulators.
+// Quantized tiles of one KV head: item i < nwt is window-old group i (slots
+// sink + 32 i ..), item nwt is the sink group (`sink` real tokens at slots
+// 0..sink-1; the cheapest tile, so it comes last in the queue).  MIXED: the
+// wave also holds fp16-tile accumulators.
 template <bool MIXED>
 struct QItems {
   typedef QTileRaw Raw;
   typedef QRef State;
   QRegion sinkq, winq;
-  int n, sink;
+  int n, sink;   // n = nwt + 1
   __device__ __forceinline__ void load(int i, Raw& X, int lane) const {
-    const bool s = i == 0;
+    const bool s = i == n - 1;
     QRegion Q;
     Q.kp = s ? sinkq.kp : winq.kp;
     Q.ks = s ? sinkq.ks : winq.ks;
@@ -112,11 +113,11 @@ struct QItems {
     Q.vp = s ? sinkq.vp : winq.vp;
     Q.vs = s ? sinkq.vs : winq.vs;
     Q.vz = s ? sinkq.vz : winq.vz;
-    load_q_raw(Q, s ? 0 : i - 1, i < n, lane, X);
+    load_q_raw(Q, s ? 0 : i, i < n, lane, X);
   }
   __device__ __forceinline__ void step(int i, const Raw& X, State& s, const StepCtx& c) const {
-    const bool sk = i == 0;
-    q_tile_step<MIXED>(X, c.slot, c.qB, sk ? 0 : sink + kTile * (i - 1), sk ? sink : kTile, c.R,
+    const bool sk = i == n - 1;
+    q_tile_step<MIXED>(X, c.slot, c.qB, sk ? 0 : sink + kTile * i, sk ? sink : kTile, c.R,
                        c.scale_log2, s.st, s.qs, c.lane);
   }
 };

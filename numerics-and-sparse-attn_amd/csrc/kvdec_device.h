@@ -67,12 +67,11 @@ __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ half8 as_h8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 __device__ __forceinline__ u32x4 as_u4(half8 v) { return __builtin_bit_cast(u32x4, v); }
 
-// a - b on two fp16 lanes in one v_pk_add_f16 (with negated b); written out
-// because the compiler splits fp16 vector subtraction into scalar halves.
+// a - b on the two fp16 halves of a dword.  Written as a 2-wide vector
+// subtraction on its own so it stays one v_pk_add_f16 (subtracting 8-wide
+// vectors is split into scalar halves by the compiler).
 __device__ __forceinline__ uint32_t pk_sub_f16(uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_pk_add_f16 %0, %1, %2 neg_lo:[0,1] neg_hi:[0,1]" : "=v"(r) : "v"(a), "v"(b));
-  return r;
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) - __builtin_bit_cast(half2v, b));
 }
 
 __device__ __forceinline__ float4v mfma16x16x32(u32x4 a, half8 b, float4v c) {
@@ -358,8 +357,10 @@ __device__ __forceinline__ uint32_t codes_1024(uint32_t c, uint32_t sel) {
 //   softmax: the reference max is refreshed whenever the tile's max exceeds
 //       it, so p <= 1 and P' = p * vscale stays within the fp16 range.
 // MIXED: the wave also holds fp16-tile accumulators in `st`, which a max
-// refresh rescales too.  Masked tokens get p = 0; their codes are finite.
-template <bool MIXED>
+// refresh rescales too.  HALF: only tokens 0..15 can be valid (the sink
+// group), so the second 16-token block is skipped in QK and fed as zeros to
+// PV.  Masked tokens get p = 0; their codes are finite.
+template <bool MIXED, bool HALF>
 __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[4], int slot0,
                                             int xlim, const SlotRanges& R, float scale_log2,
                                             WaveState& st, QState& qs, int lane) {
@@ -381,7 +382,7 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
+    for (int blk = 0; blk < (HALF ? 1 : 2); ++blk) {
       const u32x2 w =
           *reinterpret_cast<const u32x2*>(slot + kQsK + (4 * blk + (t >> 2)) * 128 + 32 * c + 8 * g);
       const uint32_t c0 = (w[0] >> sh) & 0x03030303u;
@@ -459,12 +460,14 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   for (int blk = 0; blk < 8; ++blk) {
     const char* row = slot + kQsV + (4 * blk + (t >> 2)) * 32;
     const uint32_t c0 = (*reinterpret_cast<const uint32_t*>(row + 4 * g) >> sh) & 0x03030303u;
-    const uint32_t c1 = (*reinterpret_cast<const uint32_t*>(row + 16 + 4 * g) >> sh) & 0x03030303u;
     const u32x4 z = vz1[blk >> 1];
-    const u32x4 b = {pk_sub_f16(codes_1024(c0, 0x00050004u), z[0]),
-                     pk_sub_f16(codes_1024(c0, 0x00070006u), z[1]),
-                     pk_sub_f16(codes_1024(c1, 0x00050004u), z[2]),
-                     pk_sub_f16(codes_1024(c1, 0x00070006u), z[3])};
+    u32x4 b = {pk_sub_f16(codes_1024(c0, 0x00050004u), z[0]),
+               pk_sub_f16(codes_1024(c0, 0x00070006u), z[1]), 0u, 0u};
+    if (!HALF) {
+      const uint32_t c1 = (*reinterpret_cast<const uint32_t*>(row + 16 + 4 * g) >> sh) & 0x03030303u;
+      b[2] = pk_sub_f16(codes_1024(c1, 0x00050004u), z[2]);
+      b[3] = pk_sub_f16(codes_1024(c1, 0x00070006u), z[3]);
+    }
     qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq[blk >> 1], as_h8(b), qs.O[blk], 0, 0, 0);
   }
 }
@@ -475,7 +478,10 @@ __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
                                             const SlotRanges& R, float scale_log2, WaveState& st,
                                             QState& qs, int lane) {
   stage_q_raw(raw, slot, lane);
-  q_tile_body<MIXED>(slot, qB, slot0, xlim, R, scale_log2, st, qs, lane);
+  if (xlim <= kTile / 2)
+    q_tile_body<MIXED, true>(slot, qB, slot0, xlim, R, scale_log2, st, qs, lane);
+  else
+    q_tile_body<MIXED, false>(slot, qB, slot0, xlim, R, scale_log2, st, qs, lane);
 }
 
 }  // namespace kvdec
