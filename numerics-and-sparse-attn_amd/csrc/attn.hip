@@ -86,6 +86,13 @@ struct F16Items {
   __device__ __forceinline__ void step(int i, const Raw& X, State& st, const StepCtx& c) const {
     f16_tile_step(X, c.slot, c.qB, slot_base + kTile * (tile0 + i), c.R, c.scale_log2, st, c.lane);
   }
+  // The same, in a wave whose quantized-tile accumulators qs share st.m.
+  __device__ __forceinline__ void step(int i, const Raw& X, State& st, QState& qs,
+                                       const StepCtx& c) const {
+    const int lane = c.lane;
+    f16_tile_step(X, c.slot, c.qB, slot_base + kTile * (tile0 + i), c.R, c.scale_log2, st, lane,
+                  [&](float alpha) { q_state_rescale(qs, alpha, lane); });
+  }
 };
 
 // The accumulators a quantized tile updates.
@@ -402,18 +409,21 @@ struct KiviSrc {
       rit.slot_base = sink + win_tok;
       bool has_q = false;
       if (nqw > 0) {
-        // one residual tile and (if there is one) one extra quantized tile
-        F16Raw R;
+        // one extra quantized tile (if there is one) and one residual tile.
+        // The residual tile's loads are issued after the workgroup barrier,
+        // behind the loads of every quantized tile: a CU serves its loads
+        // roughly in issue order, and the quantized steps are the long ones.
         QTileRaw E;
-        rit.load(rw, R, lane);
         const int qe = nqw + rw;
         qit.load(qe, E, lane);
-        sync(c, dyn);
-        rit.step(rw, R, st, c);
+        sync(c, true);
+        F16Raw R;
+        rit.load(rw, R, lane);
         if (qe < qit.n) {
           qit.step(qe, E, qref, c);
           has_q = true;
         }
+        rit.step(rw, R, st, qs, c);
       } else {
         Ring<F16Items> rring;
         ring_begin(rit, rring, rw, rw + nrw, lane);
@@ -439,7 +449,7 @@ struct KiviSrc {
     } else {
       Ring<QItems<false>> qring;
       ring_begin(qonly, qring, qw, qw + nqw + nrw, lane);
-      sync(c, dyn);
+      sync(c, dyn || nqw > 0);
       if (dyn_q)
         ring_run_dynamic(qonly, qring, ctr + 1, qref, c);
       else
@@ -463,16 +473,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) 
   // Q operand of this KV head's G query heads, loaded by every wave straight
   // into MFMA B-operand order (lane (n, g): head n, channels 32c + 8g .. +7)
   // before any tile load, so no wave waits on another to start computing.
+  // Lanes of heads >= G read past the resource: zeros, no memory access.
   half8 qB[4];
   {
     const int n = lane & 15, g = lane >> 4;
-    const u32x4* qp = reinterpret_cast<const u32x4*>(
-                          P.q + ((size_t)b * P.H + (size_t)kvh * P.G + min(n, P.G - 1)) * kHeadDim) + g;
+    const rsrc_t rq = make_rsrc(P.q + ((size_t)b * P.H + (size_t)kvh * P.G) * kHeadDim,
+                                (uint32_t)P.G * kRowBytes);
+    const uint32_t qoff = n < P.G ? (uint32_t)n * kRowBytes + 16u * (uint32_t)g : kOOB;
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const u32x4 v = qp[4 * cc];
-      qB[cc] = as_h8(n < P.G ? v : u32x4{0u, 0u, 0u, 0u});
-    }
+    for (int cc = 0; cc < 4; ++cc)
+      qB[cc] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 64u * cc, 0, 0));
   }
 
   int* ctr = reinterpret_cast<int*>(lds + kLdsCtr);

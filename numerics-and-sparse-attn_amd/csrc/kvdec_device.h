@@ -146,9 +146,12 @@ __device__ __forceinline__ uint32_t tile_valid_bits(const SlotRanges& R, int slo
 //                          of token tau(g, j)
 // FULL: every token of the tile is valid.  Otherwise bit j of `valid` says
 // whether the lane's token tau(g, j) is, and masked logits become -inf.
-template <bool FULL, class KOp, class VOp>
+// resc(alpha) rescales any other accumulators that share st.m (alpha per
+// head, in lane layout) when the reference max is refreshed.
+template <bool FULL, class KOp, class VOp, class Resc>
 __device__ __forceinline__ void tile_body(KOp&& kop, VOp&& vop, uint32_t valid,
-                                          const half8 (&qB)[4], float scale_log2, WaveState& st) {
+                                          const half8 (&qB)[4], float scale_log2, WaveState& st,
+                                          Resc&& resc) {
   float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -176,6 +179,7 @@ __device__ __forceinline__ void tile_body(KOp&& kop, VOp&& vop, uint32_t valid,
     st.l *= alpha;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) st.O[jj] = st.O[jj] * alpha;
+    resc(alpha);
     st.m = mnew;
   }
 
@@ -237,11 +241,16 @@ __device__ __forceinline__ uint32_t kslot_off(uint32_t row, uint32_t chunk) {
   return row * kRowBytes + 16u * (chunk ^ (row & 15u));
 }
 
+struct NoRescale {
+  __device__ __forceinline__ void operator()(float) const {}
+};
+
 // Consume an fp16 tile.  V rows of masked tokens are replaced by zeros at use
 // time: unwritten cache slots may hold anything, including non-finite values.
+template <class Resc = NoRescale>
 __device__ __forceinline__ void f16_tile_step(const F16Raw& X, char* slot, const half8 (&qB)[4],
                                               int slot0, const SlotRanges& R, float scale_log2,
-                                              WaveState& st, int lane) {
+                                              WaveState& st, int lane, Resc&& resc = Resc()) {
   const uint32_t t = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -250,11 +259,11 @@ __device__ __forceinline__ void f16_tile_step(const F16Raw& X, char* slot, const
     return *reinterpret_cast<const u32x4*>(slot + kslot_off(16u * blk + t, 4u * c + g));
   };
   if (tile_fully_valid(R, slot0)) {
-    tile_body<true>(kop, [&](int w, int j) { return X.v[j][w]; }, 0u, qB, scale_log2, st);
+    tile_body<true>(kop, [&](int w, int j) { return X.v[j][w]; }, 0u, qB, scale_log2, st, resc);
   } else {
     const uint32_t valid = tile_valid_bits(R, slot0, kTile, lane);
     tile_body<false>(kop, [&](int w, int j) { return ((valid >> j) & 1u) ? X.v[j][w] : 0u; },
-                     valid, qB, scale_log2, st);
+                     valid, qB, scale_log2, st, resc);
   }
 }
 
@@ -312,6 +321,17 @@ struct QState {
 __device__ __forceinline__ void q_state_init(QState& qs) {
 #pragma unroll
   for (int b = 0; b < 8; ++b) qs.O[b] = float4v{0.f, 0.f, 0.f, 0.f};
+}
+
+// Rescale by alpha, given per head in lane layout (head = lane & 15); the
+// rows of qs.O are heads 4g + r.
+__device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lane) {
+  const int g = lane >> 4;
+  float4v ar;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) qs.O[b] = qs.O[b] * ar;
 }
 
 // Layout of a staged KIVI tile inside a wave slot (bytes):
@@ -420,12 +440,7 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) st.O[jj] = st.O[jj] * alpha;
     }
-    // qs.O rows are heads 4g + r
-    float4v ar;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) qs.O[b] = qs.O[b] * ar;
+    q_state_rescale(qs, alpha, lane);
     st.m = mnew;
   }
   half8 pB;
