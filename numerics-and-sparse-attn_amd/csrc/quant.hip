@@ -5,13 +5,26 @@
 //   s = (mx - mn) / 3;  s = (s == 0) ? 1 : s;  z = floor(-mn / s + 0.5)
 //   code = clamp(floor(x / s + 0.5) + z, 0, 3)
 // so this file is compiled with -ffp-contract=off and keeps the HIP default
-// of correctly rounded fp32 division.  The per-element quotient fl32(x / s)
-// is computed as RN32(RN64(x * RN64(1 / s))): the fp64 product is within
-// 2^-52 (relative) of x / s, while a quotient of two 24-bit significands
-// that is not exactly a float32 rounding midpoint lies at least ~2^-48
-// (relative) away from one, so rounding the fp64 product to float32 gives
-// exactly the correctly rounded float32 quotient, for a multiply instead of
-// a full division per element.
+// of correctly rounded fp32 division for the per-group quantities.
+//
+// The per-element quotient fl32(x / s) takes three fp32 operations
+// (Markstein's division): with y = fl32(1 / s) correctly rounded and
+// q0 = fl32(x * y), which is within one ulp of x / s, the residual
+// r = x - q0 * s is exact in one FMA and fl32(q0 + r * y) is the correctly
+// rounded quotient.  The theorem needs y normal and r exact: groups whose
+// scale lies outside [2^-40, 2^100] (and groups with infinite inputs, whose
+// scale is infinite) take the slow path below instead.  Inside that range
+// every residual that matters is a normal number: r is a multiple of
+// ulp(q0) * ulp(s) / 2, which stays >= 2^-115 while |x / s| >= 2^-28, and a
+// quotient below 2^-28 cannot move floor(q + 0.5).
+//
+// Slow path: fl32(x / s) as RN32(RN64(x * RN64(1 / s))).  The fp64 product
+// is within 2^-52 (relative) of x / s, while a quotient of two 24-bit
+// significands that is not exactly a float32 rounding midpoint lies at
+// least ~2^-48 (relative) away from one, so rounding it to float32 gives the
+// correctly rounded quotient for any finite s.
+
+#include <type_traits>
 
 #include "kvdec_device.h"
 #include "kvdec.h"
@@ -22,52 +35,55 @@ namespace {
 
 constexpr int kGroup = 32;
 
-// Two adjacent elements (one 4- or 8-byte load).
-__device__ __forceinline__ void load2(const float* p, float& a, float& b) {
-  const float2 v = *reinterpret_cast<const float2*>(p);
-  a = v.x;
-  b = v.y;
-}
-__device__ __forceinline__ void load2(const _Float16* p, float& a, float& b) {
-  const half2v v = *reinterpret_cast<const half2v*>(p);
-  a = (float)v[0];
-  b = (float)v[1];
-}
-__device__ __forceinline__ void load2(const uint16_t* p, float& a, float& b) {
-  const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
-  a = __builtin_bit_cast(float, v << 16);
-  b = __builtin_bit_cast(float, v & 0xffff0000u);
-}
+// Input formats.  Raw data stays in the loaded dwords (two elements per
+// dword for the 16-bit formats) until each element is needed as a float.
+template <typename T>
+struct Fmt;
+// elem() returns an element in a type that converts exactly to float (the
+// code computation converts it where it is used, so the fp16 conversions fold
+// into mixed-precision FMAs).
+template <>
+struct Fmt<float> {
+  static constexpr int kPerWord = 1;
+  __device__ static float elem(uint32_t w, int) { return __builtin_bit_cast(float, w); }
+  __device__ static float get(uint32_t w, int i) { return elem(w, i); }
+};
+template <>
+struct Fmt<_Float16> {
+  static constexpr int kPerWord = 2;
+  __device__ static _Float16 elem(uint32_t w, int i) { return __builtin_bit_cast(half2v, w)[i]; }
+  __device__ static float get(uint32_t w, int i) { return (float)elem(w, i); }
+};
+template <>
+struct Fmt<uint16_t> {   // bfloat16
+  static constexpr int kPerWord = 2;
+  __device__ static float elem(uint32_t w, int i) {
+    return __builtin_bit_cast(float, i ? (w & 0xffff0000u) : (w << 16));
+  }
+  __device__ static float get(uint32_t w, int i) { return elem(w, i); }
+};
 
-// 32 contiguous elements (16-byte loads; the group start is 64-byte aligned
-// for 16-bit inputs and 128-byte aligned for fp32).
-__device__ __forceinline__ void load32(const float* p, float (&a)[32]) {
+// Exact min / max of element i over n words (a min or max of fp16 values is
+// one of them, so the packed fp16 reduction is exact).
+template <typename T, int N, int STRIDE>
+__device__ __forceinline__ void minmax(const uint32_t* w, int i, float& mn, float& mx) {
+  mn = mx = Fmt<T>::get(w[0], i);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 v = reinterpret_cast<const float4*>(p)[i];
-    a[4 * i] = v.x;
-    a[4 * i + 1] = v.y;
-    a[4 * i + 2] = v.z;
-    a[4 * i + 3] = v.w;
+  for (int k = 1; k < N; ++k) {
+    const float v = Fmt<T>::get(w[k * STRIDE], i);
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
   }
 }
-__device__ __forceinline__ void load32(const _Float16* p, float (&a)[32]) {
+// Both halves of N packed fp16 words at once.
+template <int N>
+__device__ __forceinline__ void minmax_h2(const uint32_t* w, half2v& mn, half2v& mx) {
+  mn = mx = __builtin_bit_cast(half2v, w[0]);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const half8 v = as_h8(reinterpret_cast<const u32x4*>(p)[i]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) a[8 * i + j] = (float)v[j];
-  }
-}
-__device__ __forceinline__ void load32(const uint16_t* p, float (&a)[32]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      a[8 * i + 2 * j] = __builtin_bit_cast(float, v[j] << 16);
-      a[8 * i + 2 * j + 1] = __builtin_bit_cast(float, v[j] & 0xffff0000u);
-    }
+  for (int k = 1; k < N; ++k) {
+    const half2v v = __builtin_bit_cast(half2v, w[k]);
+    mn = __builtin_elementwise_min(mn, v);
+    mx = __builtin_elementwise_max(mx, v);
   }
 }
 
@@ -78,71 +94,269 @@ __device__ __forceinline__ void group_params(float mn, float mx, float& s, float
   z = floorf(-mn / s + 0.5f);
 }
 
-// code = clamp(floor(fl32(x / s) + 0.5) + z, 0, 3) with fl32(x / s) from
-// the fp64 reciprocal (see file header).
-__device__ __forceinline__ uint32_t quant_code(float x, double rinv, float z) {
-  const float qv = (float)((double)x * rinv);
-  float c = floorf(qv + 0.5f) + z;
-  c = fminf(fmaxf(c, 0.0f), 3.0f);
-  return (uint32_t)c;
+// Per-group constants of the code computation.
+struct QParams {
+  float s, y, z;   // scale, fl32(1 / s), zero
+  double rinv;     // RN64(1 / s), slow path
+  bool fast;
+};
+
+__device__ __forceinline__ QParams make_params(float mn, float mx) {
+  QParams q;
+  group_params(mn, mx, q.s, q.z);
+  q.fast = q.s >= 0x1p-40f && q.s <= 0x1p100f;
+  q.y = 1.0f / q.s;
+  q.rinv = 1.0 / (double)q.s;
+  return q;
 }
 
-// K: one thread owns two adjacent channels of one 32-token group.
-//   unit = ((pair * groups) + grp) * chunks + chunk,  chunk = 128-channel slice
+// clamp(floor(fl32(x / s) + 0.5) + z, 0, 3) as a float (see file header).
+// E is float or _Float16.  q0 is formed as fma(x, y, +0), equal to fl32(x * y)
+// up to the sign of a zero (which cannot change a code), so that a 16-bit x
+// enters both FMAs unconverted.  The slow path converts x to double
+// directly, which keeps the two paths from sharing a converted copy of x.
+template <bool FAST, typename E>
+__device__ __forceinline__ float quant_code(E x, const QParams& q) {
+  float qv;
+  if (FAST) {
+    const float q0 = __builtin_fmaf((float)x, q.y, 0.0f);
+    const float r = __builtin_fmaf(-q0, q.s, (float)x);
+    qv = __builtin_fmaf(r, q.y, q0);
+  } else {
+    qv = (float)((double)x * q.rinv);
+  }
+  const float c = floorf(qv + 0.5f) + q.z;
+  return fminf(fmaxf(c, 0.0f), 3.0f);
+}
+
+// Replace byte `b` of `w` by the code c (an integer-valued float in [0, 3]).
+__device__ __forceinline__ uint32_t put_code(float c, uint32_t b, uint32_t w) {
+  return __builtin_amdgcn_cvt_pk_u8_f32(c, b, w);
+}
+
+// K: one lane owns two adjacent channels of one 32-token group; a wave owns
+// a 128-channel slice.  unit = pg * chunks + chunk with pg = pair * groups +
+// grp, the group's index over all (b, kv) heads: its input rows start at row
+// 32 pg, its packed rows at row 8 pg and its scales / zeros at row pg.
+// Raw: one dword per token (16-bit inputs, both channels) or two (fp32).
+template <typename T>
+struct KRaw {
+  static constexpr int kW = 2 / Fmt<T>::kPerWord;
+  uint32_t w[kGroup * kW];
+};
+
+// Wave-uniform position of a unit (chunks == 1, the usual D <= 128, needs
+// no division).
+struct KUnit {
+  int64_t pg;
+  int chunk;
+};
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+// Buffer resource over a wave-uniform range.  Base and size pass through
+// readfirstlane: otherwise the compiler may keep parts of the resource in
+// VGPRs and wrap every buffer access in a loop over distinct values.
+__device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, uint32_t bytes) {
+  const void* b = reinterpret_cast<const void*>(uniform64(reinterpret_cast<int64_t>(base)));
+  return make_rsrc(b, __builtin_amdgcn_readfirstlane(bytes));
+}
+__device__ __forceinline__ KUnit k_unit(int64_t unit, int chunks) {
+  if (chunks == 1) return KUnit{unit, 0};
+  return KUnit{unit / chunks, (int)(unit % chunks)};
+}
+
+template <typename T>
+__device__ __forceinline__ void k_load(const T* x, KUnit u, bool live, int D, int lane,
+                                       KRaw<T>& r) {
+  constexpr int kW = KRaw<T>::kW;
+  if (!live) return;
+  // the group's 32 rows as one buffer: per-lane offset in a VGPR, per-row
+  // offset in an SGPR (no 64-bit address arithmetic per load).  Lanes past
+  // D read out of range: zeros, no access, no divergent branch.
+  const int ch = u.chunk * 128 + 2 * lane;
+  const rsrc_t rs = make_rsrc_uniform(x + (size_t)u.pg * kGroup * D,
+                                      (uint32_t)(kGroup * D * sizeof(T)));
+  const uint32_t vo = ch < D ? (uint32_t)ch * sizeof(T) : kOOB, row = (uint32_t)D * sizeof(T);
+#pragma unroll
+  for (int t = 0; t < kGroup; ++t) {
+    if (kW == 1) {
+      r.w[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, vo, t * row, kStreamAux);
+    } else {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, vo, t * row, kStreamAux);
+      r.w[2 * t] = v[0];
+      r.w[2 * t + 1] = v[1];
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ auto k_elem(const KRaw<T>& r, int t, int c) {
+  if (KRaw<T>::kW == 1) return Fmt<T>::elem(r.w[t], c);
+  return Fmt<T>::elem(r.w[2 * t + c], 0);
+}
+
+template <typename T>
+__device__ __forceinline__ void k_quantize(const KRaw<T>& r, KUnit u, int D, int lane,
+                                           uint8_t* __restrict__ packed,
+                                           _Float16* __restrict__ scale,
+                                           _Float16* __restrict__ zero) {
+  // lanes past D compute codes of zeros and store out of range (dropped)
+  const int ch = u.chunk * 128 + 2 * lane;
+  const uint32_t vo = ch < D ? (uint32_t)ch : kOOB;
+  float amn, amx, bmn, bmx;
+  if (std::is_same<T, _Float16>::value) {
+    half2v mn, mx;
+    minmax_h2<kGroup>(r.w, mn, mx);
+    amn = (float)mn[0];
+    bmn = (float)mn[1];
+    amx = (float)mx[0];
+    bmx = (float)mx[1];
+  } else {
+    constexpr int kW = KRaw<T>::kW;
+    minmax<T, kGroup, kW>(r.w, 0, amn, amx);
+    minmax<T, kGroup, kW>(r.w + (kW - 1), kW == 1 ? 1 : 0, bmn, bmx);
+  }
+  const QParams qa = make_params(amn, amx), qb = make_params(bmn, bmx);
+  // byte p of each channel holds the codes of tokens 4p .. 4p + 3, LSB first
+  uint32_t rows[kGroup / 4];
+  auto codes = [&](auto fast) {
+    constexpr bool F = decltype(fast)::value;
+#pragma unroll
+    for (int p = 0; p < kGroup / 4; ++p) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 4 * p + j;
+        const uint32_t c = put_code(quant_code<F>(k_elem(r, t, 1), qb), 1,
+                                    put_code(quant_code<F>(k_elem(r, t, 0), qa), 0, 0u));
+        w |= c << (2 * j);
+      }
+      rows[p] = w;
+    }
+  };
+  // one path for the whole wave (the slow path is exact for every group)
+  if (__all(qa.fast && qb.fast))
+    codes(std::true_type());
+  else
+    codes(std::false_type());
+  const rsrc_t rp = make_rsrc_uniform(packed + (size_t)u.pg * (kGroup / 4) * D,
+                                      (uint32_t)(kGroup / 4 * D));
+#pragma unroll
+  for (int p = 0; p < kGroup / 4; ++p)
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)rows[p], rp, vo, p * D, kStreamAux);
+  const uint32_t mbytes = (uint32_t)D * 2, mo = vo == kOOB ? kOOB : 2 * vo;
+  const half2v sv = {(_Float16)qa.s, (_Float16)qb.s};
+  const half2v zv = {(_Float16)qa.z, (_Float16)qb.z};
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sv),
+                                        make_rsrc_uniform(scale + (size_t)u.pg * D, mbytes), mo, 0,
+                                        kStreamAux);
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, zv),
+                                        make_rsrc_uniform(zero + (size_t)u.pg * D, mbytes), mo, 0,
+                                        kStreamAux);
+}
+
+// Grid-stride loop over units, one wave per unit; the next unit's loads are
+// issued before the current unit is quantized.
 template <typename T>
 __global__ __launch_bounds__(256) void quantize_k_kernel(const T* __restrict__ x,
                                                          uint8_t* __restrict__ packed,
                                                          _Float16* __restrict__ scale,
                                                          _Float16* __restrict__ zero,
-                                                         int64_t n_units, int64_t groups, int64_t N,
-                                                         int D, int chunks) {
+                                                         int64_t n_units, int D, int chunks) {
   const int lane = threadIdx.x & 63;
   const int64_t stride = (int64_t)gridDim.x * (blockDim.x >> 6);
-  for (int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); unit < n_units;
-       unit += stride) {
-    const int chunk = (int)(unit % chunks);
-    const int64_t pg = unit / chunks;
-    const int64_t grp = pg % groups;
-    const int64_t pair = pg / groups;
-    const int ch = chunk * 128 + 2 * lane;
-    if (ch >= D) continue;
-    const T* xp = x + ((size_t)pair * N + (size_t)grp * kGroup) * D + ch;
-    float a[kGroup], b[kGroup];
-#pragma unroll
-    for (int t = 0; t < kGroup; ++t) load2(xp + (size_t)t * D, a[t], b[t]);
-    float amn = a[0], amx = a[0], bmn = b[0], bmx = b[0];
-#pragma unroll
-    for (int t = 1; t < kGroup; ++t) {
-      amn = fminf(amn, a[t]);
-      amx = fmaxf(amx, a[t]);
-      bmn = fminf(bmn, b[t]);
-      bmx = fmaxf(bmx, b[t]);
-    }
-    float as, az, bs, bz;
-    group_params(amn, amx, as, az);
-    group_params(bmn, bmx, bs, bz);
-    const double ar = 1.0 / (double)as, br = 1.0 / (double)bs;
-    uint8_t* pp = packed + ((size_t)pair * (N / 4) + (size_t)grp * (kGroup / 4)) * D + ch;
-#pragma unroll
-    for (int p = 0; p < kGroup / 4; ++p) {
-      uint32_t ba = 0, bb = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        ba |= quant_code(a[4 * p + j], ar, az) << (2 * j);
-        bb |= quant_code(b[4 * p + j], br, bz) << (2 * j);
-      }
-      *reinterpret_cast<uint16_t*>(pp + (size_t)p * D) = (uint16_t)(ba | (bb << 8));
-    }
-    const size_t mo = ((size_t)pair * groups + grp) * D + ch;
-    half2v sv = {(_Float16)as, (_Float16)bs};
-    half2v zv = {(_Float16)az, (_Float16)bz};
-    *reinterpret_cast<half2v*>(scale + mo) = sv;
-    *reinterpret_cast<half2v*>(zero + mo) = zv;
+  // wave-uniform (the buffer resources are built from it)
+  int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) +
+                 __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (unit >= n_units) return;
+  KRaw<T> cur;
+  KUnit u = k_unit(unit, chunks);
+  k_load(x, u, true, D, lane, cur);
+  for (; unit < n_units; unit += stride) {
+    KRaw<T> nxt;
+    const KUnit un = k_unit(unit + stride, chunks);
+    k_load(x, un, unit + stride < n_units, D, lane, nxt);
+    k_quantize(cur, u, D, lane, packed, scale, zero);
+    cur = nxt;
+    u = un;
   }
 }
 
-// V: one thread owns one (token, 32-channel group); unit = (pair*N + t)*(D/32) + grp
-// and the group's 32 inputs start at x + unit*32.
+// V: one thread owns one (token, 32-channel group); unit = (pair*N + t)*(D/32)
+// + grp and the group's 32 inputs start at x + unit*32.
+template <typename T>
+struct VRaw {
+  static constexpr int kW = kGroup / Fmt<T>::kPerWord;
+  uint32_t w[kW];
+};
+
+template <typename T>
+__device__ __forceinline__ void v_load(const T* x, int64_t u, int64_t n_units, VRaw<T>& r) {
+  if (u >= n_units) return;
+  const u32x4* p = reinterpret_cast<const u32x4*>(x + (size_t)u * kGroup);
+#pragma unroll
+  for (int i = 0; i < VRaw<T>::kW / 4; ++i) {
+    const u32x4 v = p[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.w[4 * i + j] = v[j];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ auto v_elem(const VRaw<T>& r, int c) {
+  constexpr int k = Fmt<T>::kPerWord;
+  return Fmt<T>::elem(r.w[c / k], c % k);
+}
+
+template <typename T>
+__device__ __forceinline__ void v_quantize(const VRaw<T>& r, int64_t u, uint8_t* __restrict__ packed,
+                                           _Float16* __restrict__ scale,
+                                           _Float16* __restrict__ zero) {
+  float mn, mx;
+  if (std::is_same<T, _Float16>::value) {
+    half2v hn, hx;
+    minmax_h2<VRaw<T>::kW>(r.w, hn, hx);
+    mn = fminf((float)hn[0], (float)hn[1]);
+    mx = fmaxf((float)hx[0], (float)hx[1]);
+  } else {
+    mn = mx = (float)v_elem(r, 0);
+#pragma unroll
+    for (int c = 1; c < kGroup; ++c) {
+      mn = fminf(mn, (float)v_elem(r, c));
+      mx = fmaxf(mx, (float)v_elem(r, c));
+    }
+  }
+  const QParams q = make_params(mn, mx);
+  // byte b of the 8 holds the codes of channels 4b .. 4b + 3, LSB first
+  u32x2 out;
+  auto codes = [&](auto fast) {
+    constexpr bool F = decltype(fast)::value;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) t = put_code(quant_code<F>(v_elem(r, 16 * w + 4 * b + j), q), b, t);
+        word |= t << (2 * j);
+      }
+      out[w] = word;
+    }
+  };
+  if (__all(q.fast))
+    codes(std::true_type());
+  else
+    codes(std::false_type());
+  // streaming (non-temporal) stores: outputs are not read again here
+  __builtin_nontemporal_store(out, reinterpret_cast<u32x2*>(packed) + u);
+  __builtin_nontemporal_store((_Float16)q.s, scale + u);
+  __builtin_nontemporal_store((_Float16)q.z, zero + u);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void quantize_v_kernel(const T* __restrict__ x,
                                                          uint8_t* __restrict__ packed,
@@ -150,30 +364,15 @@ __global__ __launch_bounds__(256) void quantize_v_kernel(const T* __restrict__ x
                                                          _Float16* __restrict__ zero,
                                                          int64_t n_units) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < n_units; u += stride) {
-    const T* xp = x + (size_t)u * kGroup;
-    float a[kGroup];
-    load32(xp, a);
-    float mn = a[0], mx = a[0];
-#pragma unroll
-    for (int i = 1; i < kGroup; ++i) {
-      mn = fminf(mn, a[i]);
-      mx = fmaxf(mx, a[i]);
-    }
-    float s, z;
-    group_params(mn, mx, s, z);
-    const double r = 1.0 / (double)s;
-    u32x2 out;
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) word |= quant_code(a[16 * w + i], r, z) << (2 * i);
-      out[w] = word;
-    }
-    *reinterpret_cast<u32x2*>(packed + (size_t)u * 8) = out;
-    scale[u] = (_Float16)s;
-    zero[u] = (_Float16)z;
+  int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= n_units) return;
+  VRaw<T> cur;
+  v_load(x, u, n_units, cur);
+  for (; u < n_units; u += stride) {
+    VRaw<T> nxt;
+    v_load(x, u + stride, n_units, nxt);
+    v_quantize(cur, u, packed, scale, zero);
+    cur = nxt;
   }
 }
 
@@ -225,9 +424,12 @@ int launch_status() {
   return e == hipSuccess ? KVDEC_OK : (int)e;
 }
 
+// One unit per thread (V) or wave (K) while the grid allows: the streaming
+// quantizers are fastest with the whole problem in flight as separate
+// workgroups rather than fewer, looping ones.
 unsigned grid_for(int64_t threads_needed, int block) {
   int64_t g = (threads_needed + block - 1) / block;
-  const int64_t cap = 256 * 64;   // 64 workgroups per CU on a 256-CU part, grid-stride beyond
+  const int64_t cap = (int64_t)1 << 30;   // workgroups; grid-stride beyond
   if (g > cap) g = cap;
   if (g < 1) g = 1;
   return (unsigned)g;
@@ -255,6 +457,7 @@ int kvdec_quantize_k(const void* x, int in_dtype, void* packed_u8, void* scale_f
   if (N % group != 0) return KVDEC_E_GROUP;
   if (group != kGroup) return KVDEC_E_UNSUPPORTED;
   if (D % 2 != 0) return KVDEC_E_SHAPE;
+  if ((int64_t)D * kGroup * 4 >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;   // 32-bit buffer offsets
   const int64_t pairs = B * KVH;
   const int64_t groups = N / kGroup;
   const int chunks = (D + 127) / 128;
@@ -266,13 +469,13 @@ int kvdec_quantize_k(const void* x, int in_dtype, void* packed_u8, void* scale_f
   auto* z = static_cast<_Float16*>(zero_f16);
   if (in_dtype == KVDEC_F32)
     hipLaunchKernelGGL(quantize_k_kernel<float>, dim3(grid), dim3(256), 0, st,
-                       static_cast<const float*>(x), p, s, z, n_units, groups, N, D, chunks);
+                       static_cast<const float*>(x), p, s, z, n_units, D, chunks);
   else if (in_dtype == KVDEC_F16)
     hipLaunchKernelGGL(quantize_k_kernel<_Float16>, dim3(grid), dim3(256), 0, st,
-                       static_cast<const _Float16*>(x), p, s, z, n_units, groups, N, D, chunks);
+                       static_cast<const _Float16*>(x), p, s, z, n_units, D, chunks);
   else
     hipLaunchKernelGGL(quantize_k_kernel<uint16_t>, dim3(grid), dim3(256), 0, st,
-                       static_cast<const uint16_t*>(x), p, s, z, n_units, groups, N, D, chunks);
+                       static_cast<const uint16_t*>(x), p, s, z, n_units, D, chunks);
   return launch_status();
 }
 

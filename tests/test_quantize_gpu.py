@@ -71,6 +71,37 @@ def test_quantize_coarse_grid_ties(device):
     _assert_same(_quant("quantize_v_cache", x, device), O.quantize_v(x))
 
 
+def test_quantize_scale_magnitudes(device):
+    """Groups whose scales span 1e-30 .. 1e30 (fp32 input): the kernels'
+    three-FMA quotient covers scales in [2^-40, 2^100] and an fp64 path the
+    rest; both must give the IEEE float32 codes.  Magnitudes vary per 32x32
+    block, so K and V groups see both uniform and mixed magnitudes."""
+    r = np.random.default_rng(11)
+    B, KVH, N, D = 1, 2, 512, 128
+    e = r.uniform(-30, 30, size=(B, KVH, N // 32, 1, D // 32, 1))
+    mag = np.broadcast_to(10.0 ** e, (B, KVH, N // 32, 32, D // 32, 32)).reshape(B, KVH, N, D)
+    x = (r.standard_normal((B, KVH, N, D)) * mag).astype(np.float32)
+    x[0, 0, :32, :5] = 3.0                          # constant groups (scale 0 -> 1)
+    x[0, 1, 64:96] += np.float32(1e4)               # large offsets: zero-points far from 0
+    say("quantize scale magnitudes")
+    with np.errstate(over="ignore"):                # scales above 65504 store as fp16 inf
+        want_k, want_v = O.quantize_k(x), O.quantize_v(x)
+    _assert_same(_quant("quantize_k_cache", x, device), want_k)
+    _assert_same(_quant("quantize_v_cache", x, device), want_v)
+
+
+@pytest.mark.parametrize("D", [64, 96, 192])
+@pytest.mark.parametrize("tdt", [torch.float16, torch.float32])
+def test_quantize_other_head_dims(D, tdt, device):
+    """Head dims other than 128: K runs 128-channel slices (the second slice
+    of D=192 is half empty), V any multiple of 32."""
+    x = randn((2, 3, 96, D), D)
+    xr = torch.from_numpy(x).to(tdt).float().numpy()
+    say(f"quantize D={D} dtype={tdt}")
+    _assert_same(_quant("quantize_k_cache", xr, device, tdt), O.quantize_k(xr))
+    _assert_same(_quant("quantize_v_cache", xr, device, tdt), O.quantize_v(xr))
+
+
 def test_quantize_config4_shape(device):
     """Config 4: [32, 8, 163840, 128] fp16, 4 outlier channels x10; the
     per-(b, kv) quantization is independent, so three heads spread over the
