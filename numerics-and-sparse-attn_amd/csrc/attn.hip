@@ -104,7 +104,7 @@ struct QRef {
 // Quantized tiles of one KV head: item i < nwt is window-old group i (slots
 // sink + 32 i ..), item nwt is the sink group (`sink` real tokens at slots
 // 0..sink-1; the cheapest tile, so it comes last in the queue).  MIXED: the
-// wave also holds fp16-tile accumulators.
+// wave also holds fp16-tile accumulators (and steps no fp16 tile after).
 template <bool MIXED>
 struct QItems {
   typedef QTileRaw Raw;
@@ -201,8 +201,8 @@ __device__ __forceinline__ void publish_f(const AttnCommon& P, const WaveState& 
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int c0 = 2 * (4 * g + r);
-      float4v lo = {st.O[0][r], st.O[1][r], st.O[2][r], st.O[3][r]};
-      float4v hi = {st.O[4][r], st.O[5][r], st.O[6][r], st.O[7][r]};
+      float4v lo = float4v{st.O[0][r], st.O[1][r], st.O[2][r], st.O[3][r]} * st.fs;
+      float4v hi = float4v{st.O[4][r], st.O[5][r], st.O[6][r], st.O[7][r]} * st.fs;
       *reinterpret_cast<float4v*>(slot + row_off(n, c0)) = lo;
       *reinterpret_cast<float4v*>(slot + row_off(n, c0 + 1)) = hi;
     }
@@ -210,13 +210,17 @@ __device__ __forceinline__ void publish_f(const AttnCommon& P, const WaveState& 
 }
 
 // Quantized-tile accumulators: lane (t, g) holds head 4g + r, channel
-// 16 blk + t.  All 16 head rows are written (rows of heads >= G stay inside
-// the wave's slot and the merge never reads them), so no write is
-// predicated.  ADD: the slot already holds this wave's fp16-tile rows (all
-// reads are issued before any write, so the adds wait on LDS once).
+// 16 blk + t, scaled by 1 / q_state_scale().  All 16 head rows are written
+// (rows of heads >= G stay inside the wave's slot and the merge never reads
+// them), so no write is predicated.  ADD: the slot already holds this wave's
+// fp16-tile rows (all reads are issued before any write, so the adds wait on
+// LDS once).
 template <bool ADD>
 __device__ __forceinline__ void publish_q(QState& qs, char* slot, int lane) {
   const int t = lane & 15, g = lane >> 4;
+  const float f = q_state_scale(lane);
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk) qs.O[blk] = qs.O[blk] * f;
   uint32_t off[8][4];
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk)
@@ -413,14 +417,16 @@ struct KiviSrc {
         // The residual tile's loads are issued after the workgroup barrier,
         // behind the loads of every quantized tile: a CU serves its loads
         // roughly in issue order, and the quantized steps are the long ones.
+        // The quantized tile goes first; the fp16 accumulators are still
+        // zero then, so it is stepped without them.
         QTileRaw E;
         const int qe = nqw + rw;
-        qit.load(qe, E, lane);
+        qonly.load(qe, E, lane);
         sync(c, true);
         F16Raw R;
         rit.load(rw, R, lane);
-        if (qe < qit.n) {
-          qit.step(qe, E, qref, c);
+        if (qe < qonly.n) {
+          qonly.step(qe, E, qref, c);
           has_q = true;
         }
         rit.step(rw, R, st, qs, c);

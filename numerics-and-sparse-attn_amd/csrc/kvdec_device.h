@@ -88,10 +88,14 @@ __device__ __forceinline__ int tau(int g, int j) { return 16 * (j >> 2) + 4 * g 
 //   m        : reference max of head n, identical in the four lanes of a head;
 //              starts at a finite sentinel so exp2(-inf - m) is 0, never NaN
 //   l        : this lane's share of the softmax denominator
+//   fs       : pending factor of O: max refreshes made by quantized tiles
+//              after the wave's last fp16 tile multiply fs, not the 32
+//              values of O (applied when O is published)
 struct WaveState {
   float4v O[8];
   float m;
   float l;
+  float fs;
 };
 
 constexpr float kMaxSentinel = -1e30f;
@@ -105,6 +109,7 @@ __device__ __forceinline__ void wave_state_init(WaveState& st) {
   for (int jj = 0; jj < 8; ++jj) st.O[jj] = float4v{0.f, 0.f, 0.f, 0.f};
   st.m = kMaxSentinel;
   st.l = 0.f;
+  st.fs = 1.f;
 }
 
 // Slot validity inside one KV head: s < va, or vb <= s < vc (slot numbers of
@@ -310,10 +315,12 @@ __device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, bool valid,
 // share).  The PV product of a quantized tile is computed transposed,
 // O[head][channel] = P'[head][token] . (code - zero)[token][channel], with
 // each MFMA covering 16 channels of one 32-channel V quantization group, so
-// the per-token V scale folds into P' = p * scale and the B operand is the
-// exact small integer code - zero.
-//   O[blk][r] : sum_t P'[t][head 4g + r] * (code - zero)[t][channel 16 blk + t]
-//               for lane (t, g)
+// the per-token V scale folds into P' = p * scale.  The B operands are exact
+// fp16 subnormals: the code as it sits in its byte (code * 4^k, k = t % 4,
+// the channel's position in the byte) times 2^-24, and, in a second MFMA,
+// -zero * 4^k * 2^-24.
+//   O[blk][r] : 4^k 2^-24 sum_t P'[t][head 4g + r] * (code - zero)[t][channel
+//               16 blk + t] for lane (t, g); q_state_scale() is 2^24 / 4^k
 struct QState {
   float4v O[8];
 };
@@ -321,6 +328,11 @@ struct QState {
 __device__ __forceinline__ void q_state_init(QState& qs) {
 #pragma unroll
   for (int b = 0; b < 8; ++b) qs.O[b] = float4v{0.f, 0.f, 0.f, 0.f};
+}
+
+// Factor that turns the lane's accumulators into output values.
+__device__ __forceinline__ float q_state_scale(int lane) {
+  return __builtin_ldexpf(1.0f, 24 - 2 * (lane & 3));
 }
 
 // Rescale by alpha, given per head in lane layout (head = lane & 15); the
@@ -336,7 +348,7 @@ __device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lan
 
 // Layout of a staged KIVI tile inside a wave slot (bytes):
 //   [0, 1024)     K codes, 8 byte rows x 128 channels (as stored)
-//   [1024, 1280)  K scales [128], [1280, 1536) K zeros [128]
+//   [1024, 1280)  K scales [128], [1280, 1536) 1024 + K zeros [128]
 //   [1536, 2560)  V codes transposed: row b (0..31) holds code byte b of
 //                 tokens 0..31
 //   [2560, 2816)  V scales transposed [4 groups][32 tokens],
@@ -346,7 +358,7 @@ constexpr int kQsK = 0, kQsKS = 1024, kQsKZ = 1280, kQsV = 1536, kQsVS = 2560, k
 __device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
   *reinterpret_cast<u32x4*>(slot + kQsK + 16 * lane) = X.kc;
   *reinterpret_cast<uint32_t*>(slot + kQsKS + 4 * lane) = X.ks;
-  *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = X.kz;
+  *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = pk_sub_f16(X.kz, 0xe400e400u);   // + 1024
   // lane L holds code bytes 16(L%2) .. +15 of token L/2
   const int tok = lane >> 1, b0 = 16 * (lane & 1);
 #pragma unroll
@@ -374,16 +386,21 @@ __device__ __forceinline__ uint32_t codes_1024(uint32_t c, uint32_t sel) {
 //       code - zero exactly, and since min/max quantization keeps |code -
 //       zero| <= 2 except in rare groups, the product with the fp16 scale is
 //       the reference's value exactly.
-//   softmax: the reference max is refreshed whenever the tile's max exceeds
-//       it, so p <= 1 and P' = p * vscale stays within the fp16 range.
-// MIXED: the wave also holds fp16-tile accumulators in `st`, which a max
-// refresh rescales too.  HALF: only tokens 0..15 can be valid (the sink
+//   softmax: the reference max is refreshed when the tile's max exceeds it
+//       by more than `slack`: kRescaleSlack when every V scale of the tile
+//       is at most kSlackVScale (then p <= 2^8 and P' = p * vscale < 2^15
+//       stays within the fp16 range), otherwise 0 (p <= 1).
+// MIXED: the wave also holds fp16-tile accumulators in `st`; a max refresh
+// defers their rescale into st.fs (no fp16 tile may follow a MIXED step).
+// Without MIXED, st.O must be zero.  HALF: only tokens 0..15 can be valid (the sink
 // group), so the second 16-token block is skipped in QK and fed as zeros to
 // PV.  Masked tokens get p = 0; their codes are finite.
+constexpr float kSlackVScale = 128.0f;
+
 template <bool MIXED, bool HALF>
 __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[4], int slot0,
                                             int xlim, const SlotRanges& R, float scale_log2,
-                                            WaveState& st, QState& qs, int lane) {
+                                            float slack, WaveState& st, QState& qs, int lane) {
   const int t = lane & 15, g = lane >> 4;
   // scale and 1024 + zero of the lane's K channels 32c + 8g .. +7
   half8 ks[4];
@@ -391,8 +408,7 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     ks[c] = *reinterpret_cast<const half8*>(slot + kQsKS + 2 * (32 * c + 8 * g));
-    kz1[c] = as_u4(*reinterpret_cast<const half8*>(slot + kQsKZ + 2 * (32 * c + 8 * g)) +
-                   (_Float16)1024.0f);
+    kz1[c] = *reinterpret_cast<const u32x4*>(slot + kQsKZ + 2 * (32 * c + 8 * g));
   }
 
   // S[token][head] on MFMA: lane (t, g) feeds token 16 blk + t, channels
@@ -430,16 +446,13 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   float lmax = x[0];
 #pragma unroll
   for (int j = 1; j < 8; ++j) lmax = fmaxf(lmax, x[j]);
-  if (__ballot(lmax > st.m)) {
+  if (__ballot(lmax > st.m + slack)) {
     float mt = fmaxf(lmax, __shfl_xor(lmax, 16));
     mt = fmaxf(mt, __shfl_xor(mt, 32));
     const float mnew = fmaxf(st.m, mt);
     const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);   // head n (lane layout)
     st.l *= alpha;
-    if (MIXED) {
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) st.O[jj] = st.O[jj] * alpha;
-    }
+    if (MIXED) st.fs *= alpha;
     q_state_rescale(qs, alpha, lane);
     st.m = mnew;
   }
@@ -453,11 +466,13 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   }
   st.l += ls;
 
-  // P' per V group and 1024 + zero of the lane's tokens: tokens
+  // P' per V group, and -zero * 4^k * 2^-24 for the lane's tokens:
   // tau(g, 0..3) = 4g..4g+3 and tau(g, 4..7) = 16 + 4g .. +3 sit
-  // contiguously in the transposed rows.
+  // contiguously in the transposed rows.  Both products are exact (the zero
+  // is an integer of at most 11 bits).
+  const _Float16 zk = (_Float16)(-__builtin_ldexpf(1.0f, 2 * (t & 3) - 24));
   half8 pq[4];
-  u32x4 vz1[4];
+  u32x4 zz[4];
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
     const u32x2 s_lo = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 8 * g);
@@ -465,25 +480,29 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
     const u32x2 z_lo = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 8 * g);
     const u32x2 z_hi = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 32 + 8 * g);
     pq[grp] = pB * as_h8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
-    vz1[grp] = as_u4(as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]}) + (_Float16)1024.0f);
+    zz[grp] = as_u4(as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]}) * zk);
   }
 
-  // PV: lane (t, g) feeds code - zero of channel 16 blk + t for the tokens
-  // tau(g, j) (transposed code byte row 4 blk + t/4, bits 2 (t % 4)); the
-  // subtraction of 1024 + zero from 1024 + code is exact.
+  // PV: lane (t, g) feeds channel 16 blk + t of the tokens tau(g, j)
+  // (transposed code byte row 4 blk + t/4, bits 2k, 2k + 1 with k = t % 4).
+  // The masked byte goes into the low byte of an fp16 whose high byte is
+  // zero: the subnormal code * 4^k * 2^-24.  The second MFMA adds the zero
+  // term with the same factor.
+  const uint32_t vmask = 0x03030303u << sh;
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) {
     const char* row = slot + kQsV + (4 * blk + (t >> 2)) * 32;
-    const uint32_t c0 = (*reinterpret_cast<const uint32_t*>(row + 4 * g) >> sh) & 0x03030303u;
-    const u32x4 z = vz1[blk >> 1];
-    u32x4 b = {pk_sub_f16(codes_1024(c0, 0x00050004u), z[0]),
-               pk_sub_f16(codes_1024(c0, 0x00070006u), z[1]), 0u, 0u};
+    const uint32_t c0 = *reinterpret_cast<const uint32_t*>(row + 4 * g) & vmask;
+    u32x4 b = {__builtin_amdgcn_perm(c0, 0u, 0x0c050c04u), __builtin_amdgcn_perm(c0, 0u, 0x0c070c06u),
+               0u, 0u};
     if (!HALF) {
-      const uint32_t c1 = (*reinterpret_cast<const uint32_t*>(row + 16 + 4 * g) >> sh) & 0x03030303u;
-      b[2] = pk_sub_f16(codes_1024(c1, 0x00050004u), z[2]);
-      b[3] = pk_sub_f16(codes_1024(c1, 0x00070006u), z[3]);
+      const uint32_t c1 = *reinterpret_cast<const uint32_t*>(row + 16 + 4 * g) & vmask;
+      b[2] = __builtin_amdgcn_perm(c1, 0u, 0x0c050c04u);
+      b[3] = __builtin_amdgcn_perm(c1, 0u, 0x0c070c06u);
     }
     qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq[blk >> 1], as_h8(b), qs.O[blk], 0, 0, 0);
+    qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq[blk >> 1], as_h8(zz[blk >> 1]), qs.O[blk], 0, 0,
+                                                       0);
   }
 }
 
@@ -493,10 +512,14 @@ __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
                                             const SlotRanges& R, float scale_log2, WaveState& st,
                                             QState& qs, int lane) {
   stage_q_raw(raw, slot, lane);
+  // every lane holds two of the tile's 128 V scales
+  const half2v vs = __builtin_bit_cast(half2v, raw.vs);
+  const float slack =
+      __ballot(!(fmaxf((float)vs[0], (float)vs[1]) <= kSlackVScale)) ? 0.0f : kRescaleSlack;
   if (xlim <= kTile / 2)
-    q_tile_body<MIXED, true>(slot, qB, slot0, xlim, R, scale_log2, st, qs, lane);
+    q_tile_body<MIXED, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
   else
-    q_tile_body<MIXED, false>(slot, qB, slot0, xlim, R, scale_log2, st, qs, lane);
+    q_tile_body<MIXED, false>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
 }
 
 }  // namespace kvdec

@@ -90,6 +90,28 @@ def test_quantized_attention_outlier_keys(device):
     assert max_abs(o, ref) < ATTN_TOL
 
 
+@pytest.mark.parametrize("vmul", [1.0, 600.0])
+def test_quantized_attention_growing_logits(vmul, device):
+    """Logits that grow along the window (K row t scaled by 1 + t/512), so
+    the running max rises tile after tile: quantized tiles refresh it
+    lazily (up to 2^8 above it) while every V scale is <= 128, and eagerly
+    when V is scaled x600 (V scales ~1200: a lazy p * scale could overflow
+    fp16).  W=4096 gives each wave a dynamic queue of many tiles."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D, W = 4, 32, 4, 128, 4096
+    gen = torch.Generator(device=device).manual_seed(21)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    ramp = 1 + torch.arange(S + W, device=device, dtype=torch.float32) / 512
+    kc = (torch.randn(B, KVH, S + W, D, generator=gen, device=device) * ramp[:, None]).half()
+    vc = (torch.randn(B, KVH, S + W, D, generator=gen, device=device) * vmul).half()
+    say(f"kivi growing logits vmul={vmul}")
+    cache = build_quantized_kv_cache(kc, vc)
+    o = _attend(q, cache, 163840, W)
+    ref = O.quantized_attention(host(q), W - R, _host_cache(cache), SCALE)
+    assert np.all(np.isfinite(o))
+    assert max_abs(o, ref) < ATTN_TOL * vmul
+
+
 @pytest.mark.parametrize("L", [1, 3, 4, 5, 60, 200, 300, 387, 388, 389])
 def test_quantized_attention_rampup(L, device):
     """Ramp-up (seq_len <= S + W): only the slots the _kv_indices rule marks
