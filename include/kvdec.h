@@ -151,6 +151,46 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
                              void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * Decode-time KIVI cache, the write side of the fused decode (no counterpart
+ * in the reference, which builds the cache once per call:
+ * quant_kernel.py:584-622).  State per (b, kv) head: the quantized sink
+ * group, a ring of n_groups window-old groups (the layouts of
+ * kvdec_sparse_decode_kivi's k_win / v_win tensors with W - R = n_groups *
+ * group), and an fp16 residual ring of ring_cap rows (a multiple of 32,
+ * >= residual + 32).
+ *
+ * kvdec_kivi_stream_append: writes k_new / v_new [B, KVH, D] fp16 into row
+ * `row` of k_ring / v_ring [B, KVH, ring_cap, D]; when evict_block >= 0 it
+ * also quantizes ring rows [32 * evict_block, +32) (K per channel, V per
+ * token, the quantizers' exact formulas) into window-old group slot
+ * evict_slot of win[6] = {k_win_packed, k_win_scale, k_win_zero,
+ * v_win_packed, v_win_scale, v_win_zero}.  With n_groups == 0 the block is
+ * dropped.  The evicted block must not contain `row`.
+ */
+int kvdec_kivi_stream_append(const void* k_new, const void* v_new, void* k_ring,
+                             void* v_ring, void* const* win, int64_t B,
+                             int32_t KVH, int32_t D, int32_t ring_cap,
+                             int32_t row, int32_t evict_block,
+                             int32_t evict_slot, int32_t n_groups,
+                             int32_t group, int32_t bits, void* stream);
+
+/*
+ * kvdec_kivi_stream_decode: the fused decode over that state.  kivi[12] as
+ * for kvdec_sparse_decode_kivi (window-old tensors holding n_groups groups,
+ * in any order: attention does not depend on it); every sink and
+ * window-old token is attended, and residual ring rows
+ * [ring_start, ring_start + ring_count) modulo ring_cap.  Same kernel as
+ * kvdec_sparse_decode_kivi, one pass, no workspace.
+ */
+int kvdec_kivi_stream_decode(const void* q, const void* k_ring,
+                             const void* v_ring, const void* const* kivi,
+                             void* o, int64_t B, int32_t H, int32_t KVH,
+                             int32_t sink, int32_t n_groups, int32_t ring_cap,
+                             int32_t ring_start, int32_t ring_count,
+                             int32_t group, int32_t bits, float sm_scale,
+                             void* stream);
+
+/*
  * Dequantize one block_n-token tile of a K region, with the reference's
  * clamping: byte = clamp(tok_start/4 + t/4, 0, num_packed-1) (C division),
  * code = (byte >> 2*(t%4)) & 3, group = min(byte/(group/4), num_groups-1),

@@ -5,7 +5,8 @@ from __future__ import annotations
 import torch
 
 
-def require_gpu_tensor(name: str, t, dtypes=(torch.float16,), ndim: int | None = None) -> None:
+def require_gpu_tensor(name: str, t, dtypes=(torch.float16,), ndim: int | None = None,
+                       contiguous: bool = True) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
     if not t.is_cuda:
@@ -14,7 +15,7 @@ def require_gpu_tensor(name: str, t, dtypes=(torch.float16,), ndim: int | None =
         raise ValueError(f"{name} must have dtype in {[str(d) for d in dtypes]}, got {t.dtype}")
     if ndim is not None and t.dim() != ndim:
         raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
-    if not t.is_contiguous():
+    if contiguous and not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
 
 

@@ -79,8 +79,10 @@ struct F16Items {
   typedef F16Raw Raw;
   rsrc_t rk, rv;
   int tile0, n, slot_base;
+  SlotRanges R;   // loads of tiles with no valid slot are skipped
   __device__ __forceinline__ void load(int i, Raw& X, int lane) const {
-    load_f16(rk, rv, i < n ? (uint32_t)(tile0 + i) * kSlotBytes : kOOB, lane, X);
+    const bool live = i < n && tile_any_valid(R, slot_base + kTile * (tile0 + i));
+    load_f16(rk, rv, live ? (uint32_t)(tile0 + i) * kSlotBytes : kOOB, lane, X);
   }
   typedef WaveState State;
   __device__ __forceinline__ void step(int i, const Raw& X, State& st, const StepCtx& c) const {
@@ -314,6 +316,7 @@ struct F16Src {
     it.tile0 = split * P.tiles_per_split;
     it.n = min(P.tiles_per_split, P.n_tiles - it.tile0);
     it.slot_base = 0;
+    it.R = P.R;
     Ring<F16Items> ring;
     ring_begin(it, ring, wave, wave + kWaves, lane);
     StepCtx c;
@@ -411,6 +414,7 @@ struct KiviSrc {
       rit.tile0 = 0;
       rit.n = n_res();
       rit.slot_base = sink + win_tok;
+      rit.R = P.R;
       bool has_q = false;
       if (nqw > 0) {
         // one extra quantized tile (if there is one) and one residual tile.
@@ -780,6 +784,62 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
   S.win_tok = win_tok;
   S.nwt = win_tok / kTile;
   return launch_attn(P, S, true, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int kvdec_kivi_stream_decode(const void* q, const void* k_ring, const void* v_ring,
+                             const void* const* kivi, void* o, int64_t B, int32_t H, int32_t KVH,
+                             int32_t sink, int32_t n_groups, int32_t ring_cap, int32_t ring_start,
+                             int32_t ring_count, int32_t group, int32_t bits, float sm_scale,
+                             void* stream) {
+  if (!q || !k_ring || !v_ring || !kivi || !o) return KVDEC_E_NULL;
+  if (bits != 2) return KVDEC_E_BITS;
+  if (group != 32) return KVDEC_E_UNSUPPORTED;
+  int rc = check_heads(B, H, KVH, kHeadDim);
+  if (rc) return rc;
+  if (sink < 1 || sink > group || n_groups < 0) return KVDEC_E_WINDOW;
+  if (ring_cap < 2 * kTile || ring_cap % kTile != 0) return KVDEC_E_WINDOW;
+  if (ring_start < 0 || ring_start >= ring_cap || ring_count < 1 || ring_count > ring_cap)
+    return KVDEC_E_WINDOW;
+  for (int i = 0; i < 6; ++i)
+    if (!kivi[i]) return KVDEC_E_NULL;
+  if (n_groups > 0)
+    for (int i = 6; i < 12; ++i)
+      if (!kivi[i]) return KVDEC_E_NULL;
+  const int64_t win_tok = (int64_t)n_groups * group;
+  if ((int64_t)ring_cap * kRowBytes >= ((int64_t)1 << 31) || win_tok * kHeadDim >= ((int64_t)1 << 31))
+    return KVDEC_E_SHAPE;
+
+  AttnCommon P{};
+  P.q = static_cast<const _Float16*>(q);
+  P.o = static_cast<_Float16*>(o);
+  P.ws = nullptr;
+  P.pairs = B * KVH;
+  P.H = H;
+  P.KVH = KVH;
+  P.G = H / KVH;
+  P.n_tiles = (int)(1 + n_groups + ring_cap / kTile);
+  P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
+  // every sink and window-old slot is valid; ring rows [start, start + count)
+  // (mod cap) of the residual are, at slots base + row
+  const int base = sink + (int)win_tok;
+  const int end = ring_start + ring_count;
+  if (end <= ring_cap)
+    P.R = SlotRanges{base, base + ring_start, base + end};
+  else
+    P.R = SlotRanges{base + end - ring_cap, base + ring_start, base + ring_cap};
+
+  auto u8 = [&](int i) { return static_cast<const uint8_t*>(kivi[i]); };
+  auto f16 = [&](int i) { return static_cast<const _Float16*>(kivi[i]); };
+  KiviSrc S{};
+  S.kres = static_cast<const _Float16*>(k_ring);
+  S.vres = static_cast<const _Float16*>(v_ring);
+  S.res_rows = ring_cap;
+  S.sinkq = QRegion{u8(0), f16(1), f16(2), u8(3), f16(4), f16(5)};
+  S.winq = n_groups > 0 ? QRegion{u8(6), f16(7), f16(8), u8(9), f16(10), f16(11)} : S.sinkq;
+  S.sink = sink;
+  S.win_tok = (int)win_tok;
+  S.nwt = n_groups;
+  return launch_attn(P, S, true, 0, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

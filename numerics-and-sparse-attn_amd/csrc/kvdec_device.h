@@ -130,6 +130,11 @@ __device__ __forceinline__ bool tile_fully_valid(const SlotRanges& R, int slot0)
   return last < R.va || (slot0 >= R.vb && last < R.vc);
 }
 
+// True when some token of the 32-token tile starting at slot0 is valid.
+__device__ __forceinline__ bool tile_any_valid(const SlotRanges& R, int slot0) {
+  return slot0 < R.va || (slot0 + kTile > R.vb && slot0 < R.vc);
+}
+
 // Validity bits of the lane's 8 tokens tau(g, j) of the tile at slot0
 // (tokens at or past xlim do not belong to the region).
 __device__ __forceinline__ uint32_t tile_valid_bits(const SlotRanges& R, int slot0, int xlim,

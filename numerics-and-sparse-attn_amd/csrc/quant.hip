@@ -419,6 +419,92 @@ __global__ __launch_bounds__(256) void dequant_v_tile_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode-time KIVI cache: append one token per (b, kv) head to the fp16
+// residual ring and, when the ring holds a full group more than the
+// residual, quantize its oldest 32-row block into a window-old group slot.
+// One workgroup per (b, kv) head.
+// ---------------------------------------------------------------------------
+struct StreamArgs {
+  const _Float16* k_new;   // [pairs][D]
+  const _Float16* v_new;
+  _Float16* k_ring;        // [pairs][cap][D]
+  _Float16* v_ring;
+  uint8_t* kp;             // [pairs][nwg * group / 4][D]
+  _Float16* ks;            // [pairs][nwg][D]
+  _Float16* kz;
+  uint8_t* vp;             // [pairs][nwg * group][D / 4]
+  _Float16* vs;            // [pairs][nwg * group][D / group]
+  _Float16* vz;
+  int D, cap, row, blk, slot, nwg;
+};
+
+__global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
+  const int64_t pair = blockIdx.x;
+  const int D = a.D;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    a.k_ring[((size_t)pair * a.cap + a.row) * D + i] = a.k_new[(size_t)pair * D + i];
+    a.v_ring[((size_t)pair * a.cap + a.row) * D + i] = a.v_new[(size_t)pair * D + i];
+  }
+  if (a.blk < 0) return;
+  const size_t blk0 = (size_t)pair * a.cap + (size_t)a.blk * kGroup;   // first ring row of the block
+  // K: one thread per channel, its 32 tokens (per-channel group)
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float x[kGroup];
+#pragma unroll
+    for (int t = 0; t < kGroup; ++t) x[t] = (float)a.k_ring[(blk0 + t) * D + d];
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int t = 1; t < kGroup; ++t) {
+      mn = fminf(mn, x[t]);
+      mx = fmaxf(mx, x[t]);
+    }
+    const QParams q = make_params(mn, mx);
+    const size_t g = (size_t)pair * a.nwg + a.slot;
+#pragma unroll
+    for (int p = 0; p < kGroup / 4; ++p) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float c = q.fast ? quant_code<true>(x[4 * p + j], q) : quant_code<false>(x[4 * p + j], q);
+        w |= (uint32_t)c << (2 * j);
+      }
+      a.kp[(g * (kGroup / 4) + p) * D + d] = (uint8_t)w;
+    }
+    a.ks[g * D + d] = (_Float16)q.s;
+    a.kz[g * D + d] = (_Float16)q.z;
+  }
+  // V: one thread per (token, 32-channel group)
+  const int ng = D / kGroup;
+  for (int u = threadIdx.x; u < kGroup * ng; u += blockDim.x) {
+    const int t = u / ng, c = u % ng;
+    const _Float16* src = a.v_ring + (blk0 + t) * D + c * kGroup;
+    float x[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) x[i] = (float)src[i];
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int i = 1; i < kGroup; ++i) {
+      mn = fminf(mn, x[i]);
+      mx = fmaxf(mx, x[i]);
+    }
+    const QParams q = make_params(mn, mx);
+    const size_t tok = ((size_t)pair * a.nwg + a.slot) * kGroup + t;
+#pragma unroll
+    for (int b = 0; b < kGroup / 4; ++b) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float cc = q.fast ? quant_code<true>(x[4 * b + j], q) : quant_code<false>(x[4 * b + j], q);
+        w |= (uint32_t)cc << (2 * j);
+      }
+      a.vp[tok * (D / 4) + c * (kGroup / 4) + b] = (uint8_t)w;
+    }
+    a.vs[tok * ng + c] = (_Float16)q.s;
+    a.vz[tok * ng + c] = (_Float16)q.z;
+  }
+}
+
 int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? KVDEC_OK : (int)e;
@@ -501,6 +587,51 @@ int kvdec_quantize_v(const void* x, int in_dtype, void* packed_u8, void* scale_f
   else
     hipLaunchKernelGGL(quantize_v_kernel<uint16_t>, dim3(grid), dim3(256), 0, st,
                        static_cast<const uint16_t*>(x), p, s, z, n_units);
+  return launch_status();
+}
+
+int kvdec_kivi_stream_append(const void* k_new, const void* v_new, void* k_ring, void* v_ring,
+                             void* const* win, int64_t B, int32_t KVH, int32_t D, int32_t ring_cap,
+                             int32_t row, int32_t evict_block, int32_t evict_slot, int32_t n_groups,
+                             int32_t group, int32_t bits, void* stream) {
+  if (!k_new || !v_new || !k_ring || !v_ring) return KVDEC_E_NULL;
+  if (bits != 2) return KVDEC_E_BITS;
+  if (group != kGroup) return KVDEC_E_UNSUPPORTED;
+  if (B < 1 || KVH < 1 || D < 1 || B * (int64_t)KVH > 0x7fffffffLL) return KVDEC_E_SHAPE;
+  if (D % kGroup != 0) return KVDEC_E_DGROUP;
+  if (ring_cap < 2 * kGroup || ring_cap % kGroup != 0) return KVDEC_E_WINDOW;
+  if (row < 0 || row >= ring_cap || n_groups < 0) return KVDEC_E_SHAPE;
+  if (evict_block >= 0) {
+    if (evict_block >= ring_cap / kGroup || row / kGroup == evict_block) return KVDEC_E_SHAPE;
+    if (n_groups > 0) {
+      if (!win) return KVDEC_E_NULL;
+      for (int i = 0; i < 6; ++i)
+        if (!win[i]) return KVDEC_E_NULL;
+      if (evict_slot < 0 || evict_slot >= n_groups) return KVDEC_E_SHAPE;
+    }
+  }
+  StreamArgs a{};
+  a.k_new = static_cast<const _Float16*>(k_new);
+  a.v_new = static_cast<const _Float16*>(v_new);
+  a.k_ring = static_cast<_Float16*>(k_ring);
+  a.v_ring = static_cast<_Float16*>(v_ring);
+  a.D = D;
+  a.cap = ring_cap;
+  a.row = row;
+  // a window == residual cache has no window-old groups: the block is dropped
+  a.blk = (evict_block >= 0 && n_groups > 0) ? evict_block : -1;
+  a.slot = evict_slot;
+  a.nwg = n_groups;
+  if (a.blk >= 0) {
+    a.kp = static_cast<uint8_t*>(win[0]);
+    a.ks = static_cast<_Float16*>(win[1]);
+    a.kz = static_cast<_Float16*>(win[2]);
+    a.vp = static_cast<uint8_t*>(win[3]);
+    a.vs = static_cast<_Float16*>(win[4]);
+    a.vz = static_cast<_Float16*>(win[5]);
+  }
+  hipLaunchKernelGGL(stream_append_kernel, dim3((unsigned)(B * KVH)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
   return launch_status();
 }
 

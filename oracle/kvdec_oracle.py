@@ -374,6 +374,34 @@ def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=128, sink=4
     return out
 
 
+def stream_cache(k_full, v_full, prefill_len, seq_len, window, sink=4, residual_size=128,
+                 group_size=32):
+    """Expected contents of the decode-time KIVI cache after a prefill of
+    ``prefill_len`` tokens and ``seq_len - prefill_len`` single-token appends.
+
+    The reference has no streaming cache; its builder (quant_kernel.py:584-622,
+    ``build_quantized_kv_cache`` above) is this state right after an eviction.
+    Semantics: after e = (seq_len - prefill_len) // group evictions the
+    residual holds positions [prefill_len - residual_size + group * e,
+    seq_len) (residual_size .. residual_size + group - 1 tokens), the
+    window-old groups the (window - residual_size) positions before that, in
+    group-aligned blocks, and the sink the first ``sink`` positions.  So the
+    state is the builder's output on the compacted cache sink + [window-old
+    start, seq_len) with the residual length extended by the pending tokens.
+    Returns (14-key dict with window-old in position order, win_old_len).
+    k_full, v_full: [B, KVH, >= seq_len, D] (positions 0..).
+    """
+    L0, L = int(prefill_len), int(seq_len)
+    e = (L - L0) // group_size
+    res_start = L0 - residual_size + group_size * e
+    wo_start = res_start - (window - residual_size)
+    comp_k = np.concatenate([k_full[:, :, :sink], k_full[:, :, wo_start:L]], axis=2)
+    comp_v = np.concatenate([v_full[:, :, :sink], v_full[:, :, wo_start:L]], axis=2)
+    cache = build_quantized_kv_cache(comp_k, comp_v, residual_size=L - res_start, sink=sink,
+                                     group_size=group_size)
+    return cache, window - residual_size
+
+
 def dequantized_regimes(cache, win_old_len, sink=4, group_size=32):
     """Dequantized K and V of the whole [sink + W] cache, in slot order.
 

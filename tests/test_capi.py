@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 11
+    assert len(funcs) == 13
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -178,6 +178,52 @@ def test_quantize_validation(name):
         assert _quant(fn, D=7) == E["SHAPE"]
     else:
         assert _quant(fn, D=100) == E["DGROUP"]
+
+
+def _append(**kw):
+    a = dict(kn=FAKE, vn=FAKE, kr=FAKE, vr=FAKE, win=[0x1000] * 6, B=32, KVH=8, D=128, cap=160,
+             row=0, blk=-1, slot=0, ng=4, group=32, bits=2, stream=None)
+    a.update(kw)
+    arr = (K._vp * 6)(*a["win"]) if a["win"] is not None else None
+    return K.lib.kvdec_kivi_stream_append(a["kn"], a["vn"], a["kr"], a["vr"], arr, a["B"], a["KVH"],
+                                          a["D"], a["cap"], a["row"], a["blk"], a["slot"], a["ng"],
+                                          a["group"], a["bits"], a["stream"])
+
+
+def test_stream_append_validation():
+    assert _append(kn=None) == E["NULL"]
+    assert _append(bits=4) == E["BITS"]
+    assert _append(group=64) == E["UNSUPPORTED"]
+    assert _append(D=100) == E["DGROUP"]
+    assert _append(cap=32) == E["WINDOW"]            # below residual + one group
+    assert _append(cap=170) == E["WINDOW"]
+    assert _append(row=160) == E["SHAPE"]
+    assert _append(blk=5) == E["SHAPE"]
+    assert _append(row=40, blk=1) == E["SHAPE"]      # the evicted block holds the new row
+    assert _append(blk=1, slot=4) == E["SHAPE"]
+    assert _append(blk=1, win=[0x1000] * 5 + [None]) == E["NULL"]
+    assert _append(blk=1, win=None) == E["NULL"]
+
+
+def _sdecode(**kw):
+    a = dict(q=FAKE, kr=FAKE, vr=FAKE, o=FAKE, B=32, H=64, KVH=8, S=4, ng=4, cap=160, start=0,
+             count=128, group=32, bits=2, scale=0.088, stream=None)
+    a.update(kw)
+    arr = (K._vp * 12)(*([0x1000] * 12))
+    return K.lib.kvdec_kivi_stream_decode(a["q"], a["kr"], a["vr"], arr, a["o"], a["B"], a["H"],
+                                          a["KVH"], a["S"], a["ng"], a["cap"], a["start"], a["count"],
+                                          a["group"], a["bits"], a["scale"], a["stream"])
+
+
+def test_stream_decode_validation():
+    assert _sdecode(q=None) == E["NULL"]
+    assert _sdecode(bits=3) == E["BITS"]
+    assert _sdecode(S=0) == E["WINDOW"]
+    assert _sdecode(cap=48) == E["WINDOW"]
+    assert _sdecode(start=160) == E["WINDOW"]
+    assert _sdecode(count=0) == E["WINDOW"]
+    assert _sdecode(count=161) == E["WINDOW"]
+    assert _sdecode(KVH=3) == E["SHAPE"]
 
 
 def test_dequant_tile_validation():

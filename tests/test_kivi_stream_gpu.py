@@ -1,0 +1,95 @@
+"""Decode-time KIVI cache (kivi_stream.py) on the GPU: appends with
+quantize-on-evict, then the fused decode over the ring state.
+
+Right after each eviction the state must be what the reference's builder
+(quant_kernel.py:584-622) makes of the compacted cache at that length: the
+same window-old codes (bit-exact, in ring order), the same residual tokens,
+and the same decode output as the one-shot path.  Between evictions the
+output is checked against the CPU oracle's stream_cache state."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import ATTN_TOL, SCALE, dev, host, max_abs, say
+from oracle import kvdec_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+S, R, G = 4, 128, 32
+
+
+def _stream(B, H, KVH, W, L0, steps, seed):
+    from kivi_stream import KiviStreamCache
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    D = 128
+    kf = torch.randn(B, KVH, L0 + steps, D, generator=gen, device="cuda", dtype=torch.float16)
+    vf = torch.randn(B, KVH, L0 + steps, D, generator=gen, device="cuda", dtype=torch.float16)
+    q = torch.randn(B, H, D, generator=gen, device="cuda", dtype=torch.float16)
+    cache = KiviStreamCache.from_prefill(kf[:, :, :L0], vf[:, :, :L0], W)
+    return cache, kf, vf, q
+
+
+@pytest.mark.parametrize("W", [256, 1024, 128])
+def test_stream_matches_builder_after_evictions(W, device):
+    from quant_kernel import build_quantized_kv_cache, sparse_decode_attention_quantized
+    B, H, KVH = 4, 32, 4
+    L0 = S + W + 37
+    cache, kf, vf, q = _stream(B, H, KVH, W, L0, 3 * G, 40 + W)
+    for step in range(3 * G):
+        cache.append(kf[:, :, cache.seq_len], vf[:, :, cache.seq_len])
+        if cache.ring.count != R:
+            continue
+        L = cache.seq_len
+        say(f"stream W={W} L={L}")
+        comp_k = torch.cat([kf[:, :, :S], kf[:, :, L - W:L]], dim=2)
+        comp_v = torch.cat([vf[:, :, :S], vf[:, :, L - W:L]], dim=2)
+        ref = build_quantized_kv_cache(comp_k, comp_v)
+        o_ref = sparse_decode_attention_quantized(
+            q, ref["k_residual"], ref["v_residual"],
+            ref["k_sink_packed"], ref["k_sink_scale"], ref["k_sink_zero"],
+            ref["v_sink_packed"], ref["v_sink_scale"], ref["v_sink_zero"],
+            ref["k_win_packed"], ref["k_win_scale"], ref["k_win_zero"],
+            ref["v_win_packed"], ref["v_win_scale"], ref["v_win_zero"], seq_len=L, window=W)
+        o = cache.attend(q)
+        torch.cuda.synchronize()
+        # window-old groups: ring slots in age order hold the builder's groups
+        slots = cache.window_old_slots()
+        for name, per in (("k_win_packed", G // 4), ("k_win_scale", 1), ("k_win_zero", 1),
+                          ("v_win_packed", G), ("v_win_scale", G), ("v_win_zero", G)):
+            got = host(cache.t[name])
+            want = host(ref[name])
+            for age, slot in enumerate(slots):
+                np.testing.assert_array_equal(got[:, :, slot * per:(slot + 1) * per],
+                                              want[:, :, age * per:(age + 1) * per], err_msg=name)
+        rows = cache.residual_rows()
+        np.testing.assert_array_equal(host(cache.t["k_ring"])[:, :, rows], host(ref["k_residual"]))
+        np.testing.assert_array_equal(host(cache.t["v_ring"])[:, :, rows], host(ref["v_residual"]))
+        for name in ("k_sink_packed", "k_sink_scale", "k_sink_zero", "v_sink_packed"):
+            np.testing.assert_array_equal(host(cache.t[name]), host(ref[name]), err_msg=name)
+        assert max_abs(host(o), host(o_ref)) < 1e-3
+
+
+def test_stream_between_evictions_vs_oracle(device):
+    B, H, KVH, W = 2, 16, 2, 256
+    L0 = S + W + 5
+    steps = 70
+    cache, kf, vf, q = _stream(B, H, KVH, W, L0, steps, 77)
+    kh, vh, qh = host(kf), host(vf), host(q)
+    for step in range(steps):
+        cache.append(kf[:, :, cache.seq_len], vf[:, :, cache.seq_len])
+        if step % 9 != 4:
+            continue
+        L = cache.seq_len
+        say(f"stream between evictions L={L} count={cache.ring.count}")
+        o = host(cache.attend(q))
+        oc, wlen = O.stream_cache(kh, vh, L0, L, W)
+        ref = O.quantized_attention(qh, wlen, oc, SCALE)
+        assert max_abs(o, ref) < ATTN_TOL
+
+
+def test_stream_rejects_short_prefill(device):
+    from kivi_stream import KiviStreamCache
+    k = torch.zeros(1, 2, S + 255, 128, dtype=torch.float16, device=device)
+    with pytest.raises(ValueError):
+        KiviStreamCache.from_prefill(k, k, 256)
