@@ -1,6 +1,7 @@
 """Decode-attention benchmark on one MI355X: prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--paths kivi,dense,sparse,quantize,sweep]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--paths kivi,dense,sparse,quantize,sweep,stream]
                     [--no-cpu] [--no-latency]
 
 Workload (the BASELINE metric's configuration): B=32, 64 query / 8 KV heads,
@@ -14,6 +15,9 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
   quantize  KIVI quantization of the [32, 8, 163840, 128] K and V caches (config 4)
   sweep     the fused decode at W = 1024 and 4096 (config 5; W=32 < R is
             outside the reference's domain)
+  stream    a decode loop on the streaming KIVI cache (kivi_stream.py, W=256):
+            append one token (quantizing a block every 32 steps), then attend;
+            each cache advances 32 steps, so the time includes one eviction
 
 Timing.  Each path keeps several independent input sets resident in HBM
 (together >= 1 GiB, more than L2 plus the 256 MB Infinity Cache) and captures
@@ -87,6 +91,19 @@ def bytes_kivi(window, residual=R, sink_tokens=S):
     v_codes = quant_tok * D // 4
     v_meta = 2 * 2 * quant_tok * (D // 32)
     return bytes_q_o() + pairs * (2 * residual * D * 2 + k_codes + k_meta + v_codes + v_meta)
+
+
+def bytes_stream_step(window, residual=R):
+    """One decode step of the streaming KIVI cache, averaged over a group of
+    32 steps: read the new token's K/V and write it into the residual ring;
+    attend over sink + window-old + residual .. residual + 31 ring rows
+    (residual + 15.5 on average); once per 32 steps read a 32-row block and
+    write its codes and scales/zeros (K per channel, V per token)."""
+    pairs = B * KVH
+    append = pairs * 2 * 2 * D * 2
+    attend = bytes_kivi(window, residual) + pairs * 2 * 15.5 * D * 2
+    evict = pairs * (2 * 32 * D * 2 + 2 * (32 * D // 4) + 2 * 2 * D + 2 * 2 * 32 * (D // 32))
+    return int(append + attend + evict / 32)
 
 
 def bytes_quantize(n_tok):
@@ -232,7 +249,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--paths", default="kivi,dense,sparse,quantize,sweep")
+    ap.add_argument("--paths", default="kivi,dense,sparse,quantize,sweep,stream")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-latency", action="store_true", help="skip the per-call latency runs")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -305,6 +322,31 @@ def main():
     if "sweep" in paths:
         for w in (1024, 4096):
             kivi_path(w, K, f"kivi_w{w}")
+
+    if "stream" in paths:
+        # decode loop over the streaming KIVI cache (kivi_stream.py): each
+        # step appends one token (quantizing a block into the window-old ring
+        # every 32 steps) and attends; steps rotate over independent caches
+        # so that every step starts cold, and each cache advances 32 tokens
+        from kivi_stream import KiviStreamCache
+        ns = n_sets(bytes_stream_step(W))
+        caches, toks = [], []
+        for _ in range(ns):
+            kc, vc = compacted(W)
+            caches.append(KiviStreamCache.from_prefill(kc, vc, W))
+            del kc, vc
+            toks.append((randn(B, H, D), [randn(B, KVH, D) for _ in range(2)]))
+        ssteps = 32 * ns
+
+        def scall(i):
+            c = caches[i % ns]
+            q, (kn, vn) = toks[i % ns]
+            c.append(kn, vn)
+            return c.attend(q)
+
+        ms, _ = graph_time(scall, ns, ssteps, Wu)
+        out["kivi_stream_w256"] = path_record(ms, bytes_stream_step(W), ns, ssteps)
+        del caches, toks
 
     if "sparse" in paths:
         ns = n_sets(bytes_sparse(W))
