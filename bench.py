@@ -16,8 +16,9 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
   sweep     the fused decode at W = 1024 and 4096 (config 5; W=32 < R is
             outside the reference's domain)
   stream    a decode loop on the streaming KIVI cache (kivi_stream.py, W=256):
-            append one token (quantizing a block every 32 steps), then attend;
-            each cache advances 32 steps, so the time includes one eviction
+            reserve the next token's ring row (quantizing a block every 32
+            steps), then attend; each cache advances 32 steps, so the time
+            includes one eviction per 32 steps
 
 Timing.  Each path keeps several independent input sets resident in HBM
 (together >= 1 GiB, more than L2 plus the 256 MB Infinity Cache) and captures
@@ -95,12 +96,12 @@ def bytes_kivi(window, residual=R, sink_tokens=S):
 
 def bytes_stream_step(window, residual=R):
     """One decode step of the streaming KIVI cache, averaged over a group of
-    32 steps: read the new token's K/V and write it into the residual ring;
-    attend over sink + window-old + residual .. residual + 31 ring rows
-    (residual + 15.5 on average); once per 32 steps read a 32-row block and
-    write its codes and scales/zeros (K per channel, V per token)."""
+    32 steps: attend over sink + window-old + residual .. residual + 31 ring
+    rows (residual + 15.5 on average); once per 32 steps read a 32-row block
+    and write its codes and scales/zeros (K per channel, V per token).  The
+    new token's K/V are written into the ring by their producer."""
     pairs = B * KVH
-    append = pairs * 2 * 2 * D * 2
+    append = 0
     attend = bytes_kivi(window, residual) + pairs * 2 * 15.5 * D * 2
     evict = pairs * (2 * 32 * D * 2 + 2 * (32 * D // 4) + 2 * 2 * D + 2 * 2 * 32 * (D // 32))
     return int(append + attend + evict / 32)
@@ -325,9 +326,10 @@ def main():
 
     if "stream" in paths:
         # decode loop over the streaming KIVI cache (kivi_stream.py): each
-        # step appends one token (quantizing a block into the window-old ring
-        # every 32 steps) and attends; steps rotate over independent caches
-        # so that every step starts cold, and each cache advances 32 tokens
+        # step reserves the next token's ring row (quantizing a block into
+        # the window-old ring every 32 steps) and attends; steps rotate over
+        # independent caches so that every step starts cold, and each cache
+        # advances 32 tokens
         from kivi_stream import KiviStreamCache
         ns = n_sets(bytes_stream_step(W))
         caches, toks = [], []
@@ -335,14 +337,15 @@ def main():
             kc, vc = compacted(W)
             caches.append(KiviStreamCache.from_prefill(kc, vc, W))
             del kc, vc
-            toks.append((randn(B, H, D), [randn(B, KVH, D) for _ in range(2)]))
+            toks.append((randn(B, H, D),))
         ssteps = 32 * ns
 
         def scall(i):
+            # the token's K/V are written into the reserved ring row by their
+            # producer (the projection), which is not part of this step
             c = caches[i % ns]
-            q, (kn, vn) = toks[i % ns]
-            c.append(kn, vn)
-            return c.attend(q)
+            c.reserve()
+            return c.attend(toks[i % ns][0])
 
         ms, _ = graph_time(scall, ns, ssteps, Wu)
         out["kivi_stream_w256"] = path_record(ms, bytes_stream_step(W), ns, ssteps)

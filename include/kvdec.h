@@ -160,7 +160,8 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
  * >= residual + 32).
  *
  * kvdec_kivi_stream_append: writes k_new / v_new [B, KVH, D] fp16 into row
- * `row` of k_ring / v_ring [B, KVH, ring_cap, D]; when evict_block >= 0 it
+ * `row` of k_ring / v_ring [B, KVH, ring_cap, D] (both NULL: no write, the
+ * caller's producer writes the row itself); when evict_block >= 0 it
  * also quantizes ring rows [32 * evict_block, +32) (K per channel, V per
  * token, the quantizers' exact formulas) into window-old group slot
  * evict_slot of win[6] = {k_win_packed, k_win_scale, k_win_zero,

@@ -442,10 +442,11 @@ struct StreamArgs {
 __global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
   const int64_t pair = blockIdx.x;
   const int D = a.D;
-  for (int i = threadIdx.x; i < D; i += blockDim.x) {
-    a.k_ring[((size_t)pair * a.cap + a.row) * D + i] = a.k_new[(size_t)pair * D + i];
-    a.v_ring[((size_t)pair * a.cap + a.row) * D + i] = a.v_new[(size_t)pair * D + i];
-  }
+  if (a.k_new)
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+      a.k_ring[((size_t)pair * a.cap + a.row) * D + i] = a.k_new[(size_t)pair * D + i];
+      a.v_ring[((size_t)pair * a.cap + a.row) * D + i] = a.v_new[(size_t)pair * D + i];
+    }
   if (a.blk < 0) return;
   const size_t blk0 = (size_t)pair * a.cap + (size_t)a.blk * kGroup;   // first ring row of the block
   // K: one thread per channel, its 32 tokens (per-channel group)
@@ -594,7 +595,7 @@ int kvdec_kivi_stream_append(const void* k_new, const void* v_new, void* k_ring,
                              void* const* win, int64_t B, int32_t KVH, int32_t D, int32_t ring_cap,
                              int32_t row, int32_t evict_block, int32_t evict_slot, int32_t n_groups,
                              int32_t group, int32_t bits, void* stream) {
-  if (!k_new || !v_new || !k_ring || !v_ring) return KVDEC_E_NULL;
+  if (!k_ring || !v_ring || (!k_new) != (!v_new)) return KVDEC_E_NULL;
   if (bits != 2) return KVDEC_E_BITS;
   if (group != kGroup) return KVDEC_E_UNSUPPORTED;
   if (B < 1 || KVH < 1 || D < 1 || B * (int64_t)KVH > 0x7fffffffLL) return KVDEC_E_SHAPE;
@@ -620,6 +621,7 @@ int kvdec_kivi_stream_append(const void* k_new, const void* v_new, void* k_ring,
   a.row = row;
   // a window == residual cache has no window-old groups: the block is dropped
   a.blk = (evict_block >= 0 && n_groups > 0) ? evict_block : -1;
+  if (!k_new && a.blk < 0) return KVDEC_OK;   // nothing to do
   a.slot = evict_slot;
   a.nwg = n_groups;
   if (a.blk >= 0) {

@@ -12,10 +12,15 @@ module keeps the same regimes as a streaming state:
   residual    an fp16 ring of residual + 32 rows holding the most recent
               residual .. residual + 31 tokens.
 
-Each append writes the new token into the residual ring.  When the ring
-holds residual + 32 tokens, its oldest 32-row block is quantized (K per
-channel, V per token, the quantizers' exact formulas) into the slot of the
-oldest window-old group, which leaves the window.  So the attended window is
+Each new token goes into the residual ring.  When the ring holds
+residual + 32 tokens, its oldest 32-row block is quantized (K per channel,
+V per token, the quantizers' exact formulas) into the slot of the oldest
+window-old group, which leaves the window.
+
+Two ways to add a token: append(k_new, v_new) copies it in; reserve()
+returns [B, KVH, D] views of the ring row the token belongs in, so that the
+kernel producing K and V (the projection) writes them there directly and the
+decode loop costs only attend() plus one quantization every 32 tokens.  So the attended window is
 window .. window + 31 tokens: sink + every window-old group + the residual
 ring's valid rows.  Right after an eviction (residual count == residual) the
 state holds exactly what build_quantized_kv_cache builds from the compacted
@@ -117,6 +122,23 @@ class KiviStreamCache:
     def shape(self):
         B, KVH, cap, D = self.t["k_ring"].shape
         return B, KVH, D
+
+    def reserve(self):
+        """Advance by one token and return (k_view, v_view), the [B, KVH, D]
+        ring-row views to write its K and V into before the next attend().
+        A block eviction due at this token is enqueued here, before the
+        caller's writes (it never touches the returned row)."""
+        B, KVH, D = self.shape
+        row, blk, slot = self.ring.append()
+        if blk >= 0:
+            win = (K._vp * 6)(*[K.ptr(self.t[n]) if self.t[n].numel() else None for n in _WIN_KEYS])
+            rc = K.lib.kvdec_kivi_stream_append(None, None, K.ptr(self.t["k_ring"]),
+                                                K.ptr(self.t["v_ring"]), win, B, KVH, D, self.ring.cap,
+                                                row, blk, slot, self.ring.n_groups, GROUP_SIZE,
+                                                QUANT_BITS, K.stream_of(self.t["k_ring"]))
+            K.check(rc, "KiviStreamCache.reserve")
+        self.seq_len += 1
+        return self.t["k_ring"][:, :, row], self.t["v_ring"][:, :, row]
 
     def append(self, k_new, v_new):
         """Append the token at position seq_len: k_new, v_new [B, KVH, D]

@@ -191,7 +191,8 @@ def _append(**kw):
 
 
 def test_stream_append_validation():
-    assert _append(kn=None) == E["NULL"]
+    assert _append(kn=None) == E["NULL"]               # one of the pair missing
+    assert _append(kr=None) == E["NULL"]
     assert _append(bits=4) == E["BITS"]
     assert _append(group=64) == E["UNSUPPORTED"]
     assert _append(D=100) == E["DGROUP"]

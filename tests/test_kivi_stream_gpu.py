@@ -88,6 +88,24 @@ def test_stream_between_evictions_vs_oracle(device):
         assert max_abs(o, ref) < ATTN_TOL
 
 
+def test_stream_reserve_equals_append(device):
+    """reserve() + writing the row views gives the state append() gives."""
+    B, H, KVH, W = 2, 16, 2, 256
+    L0 = S + W + 3
+    a, kf, vf, q = _stream(B, H, KVH, W, L0, 40, 91)
+    from kivi_stream import KiviStreamCache
+    b = KiviStreamCache.from_prefill(kf[:, :, :L0], vf[:, :, :L0], W)
+    for step in range(40):
+        a.append(kf[:, :, a.seq_len], vf[:, :, a.seq_len])
+        kv, vv = b.reserve()
+        kv.copy_(kf[:, :, b.seq_len - 1])
+        vv.copy_(vf[:, :, b.seq_len - 1])
+    say("stream reserve vs append")
+    for name in a.t:
+        np.testing.assert_array_equal(host(a.t[name]), host(b.t[name]), err_msg=name)
+    np.testing.assert_array_equal(host(a.attend(q)), host(b.attend(q)))
+
+
 def test_stream_rejects_short_prefill(device):
     from kivi_stream import KiviStreamCache
     k = torch.zeros(1, 2, S + 255, 128, dtype=torch.float16, device=device)
