@@ -13,8 +13,8 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
   dense     dense GQA decode over all 163840 tokens (and L=32768, config 2)
   sparse    fp16 sink+window(W=256) decode (config 3)
   quantize  KIVI quantization of the [32, 8, 163840, 128] K and V caches (config 4)
-  sweep     the fused decode at W = 1024 and 4096 (config 5; W=32 < R is
-            outside the reference's domain)
+  sweep     the fused decode at W = 32, 1024 and 4096 (config 5; W=32 < R,
+            which the reference leaves undefined, keeps the window fp16)
   stream    a decode loop on the streaming KIVI cache (kivi_stream.py, W=256):
             reserve the next token's ring row (quantizing a block every 32
             steps), then attend; each cache advances 32 steps, so the time
@@ -86,6 +86,7 @@ def bytes_kivi(window, residual=R, sink_tokens=S):
     tokens.  sink_tokens=32 gives the reference's own accounting (padded sink
     group, benchmark.py:121-129)."""
     pairs = B * KVH
+    residual = min(residual, window)          # a window below the residual stays fp16
     quant_tok = sink_tokens + (window - residual)
     k_codes = quant_tok * D // 4
     k_meta = 2 * 2 * D * (-(-sink_tokens // 32) + (window - residual) // 32)
@@ -321,7 +322,7 @@ def main():
         kivi_path(W, K, "kivi_w256", with_cpu=True)
 
     if "sweep" in paths:
-        for w in (1024, 4096):
+        for w in (32, 1024, 4096):
             kivi_path(w, K, f"kivi_w{w}")
 
     if "stream" in paths:

@@ -128,7 +128,7 @@ int kvdec_quantize_v(const void* x, int in_dtype, void* packed_u8,
 /*
  * Fused sink + window + KIVI-2bit decode.  Replaces quant_kernel.py:551-581
  * (sparse_decode_attention_quantized) and quant_kernel.py:436-548.
- *   k_res, v_res : [B, KVH, residual, D] fp16 (the most recent tokens)
+ *   k_res, v_res : [B, KVH, min(window, residual), D] fp16 (the most recent tokens)
  *   kivi[12] (host array of device pointers), in this order:
  *     k_sink_packed [B,KVH,group/4,D] u8, k_sink_scale, k_sink_zero [B,KVH,1,D],
  *     v_sink_packed [B,KVH,group,D/4] u8, v_sink_scale, v_sink_zero [B,KVH,group,D/group],
@@ -137,8 +137,11 @@ int kvdec_quantize_v(const void* x, int in_dtype, void* packed_u8,
  *   (the k_win / v_win pointers may be NULL when window == residual).
  *   Slot s of the logical [sink + window] cache is sink token s (s < sink),
  *   window-old token s - sink, or residual row s - (sink + window - residual);
- *   slots are masked by _kv_indices validity.  window >= residual,
- *   (window - residual) % group == 0, residual % 32 == 0, sink <= group.
+ *   slots are masked by _kv_indices validity.  (window - residual) % group
+ *   == 0, residual % 32 == 0, sink <= group.  window < residual (left
+ *   undefined by the reference, quant_kernel.py:589-590) means the whole
+ *   window stays fp16: k_res / v_res hold the `window` window tokens and
+ *   there are no window-old tokens.
  *   Runs in one pass (one workgroup per KV head): ws / ws_bytes are
  *   accepted for interface stability and ignored (kvdec_workspace_bytes
  *   returns 0 for KVDEC_KIND_KIVI).

@@ -349,7 +349,7 @@ struct KiviSrc {
   // quantized wave (all three loaded at launch), then dynamically.  A longer
   // residual makes every wave a residual wave with a dynamic residual queue,
   // and all quantized tiles dynamic.
-  __device__ __forceinline__ int n_res() const { return res_rows / kTile; }
+  __device__ __forceinline__ int n_res() const { return (res_rows + kTile - 1) / kTile; }
   __device__ __forceinline__ int n_res_waves() const { return min(n_res(), kWaves); }
   __device__ __forceinline__ int n_static_q() const {
     const int nrw = n_res_waves(), nqw = kWaves - nrw;
@@ -574,7 +574,7 @@ Plan make_plan(int64_t pairs, int64_t n_tiles) {
 }
 
 int64_t tiles_for(int kind, int64_t n_slots) {
-  if (kind == KVDEC_KIND_KIVI) return 1 + n_slots / kTile;
+  if (kind == KVDEC_KIND_KIVI) return 1 + (n_slots + kTile - 1) / kTile;
   return (n_slots + kTile - 1) / kTile;
 }
 
@@ -742,16 +742,19 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
   int rc = check_heads(B, H, KVH, kHeadDim);
   if (rc) return rc;
   if (seq_len < 1) return KVDEC_E_SEQLEN;
-  if (sink < 1 || sink > group || residual < kTile || residual % kTile != 0 || window < residual)
+  if (sink < 1 || sink > group || residual < kTile || residual % kTile != 0 || window < 1)
     return KVDEC_E_WINDOW;
-  const int32_t win_tok = window - residual;
+  // A window shorter than the residual stays fp16 entirely (residual rows =
+  // window, no window-old tokens).
+  const int32_t res_rows = window < residual ? window : residual;
+  const int32_t win_tok = window - res_rows;
   if (win_tok % group != 0) return KVDEC_E_GROUP;
   for (int i = 0; i < 6; ++i)
     if (!kivi[i]) return KVDEC_E_NULL;
   if (win_tok > 0)
     for (int i = 6; i < 12; ++i)
       if (!kivi[i]) return KVDEC_E_NULL;
-  if ((int64_t)residual * kRowBytes >= ((int64_t)1 << 31) ||
+  if ((int64_t)res_rows * kRowBytes >= ((int64_t)1 << 31) ||
       (int64_t)win_tok * kHeadDim >= ((int64_t)1 << 31))
     return KVDEC_E_SHAPE;
   (void)ws;
@@ -774,7 +777,7 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
   KiviSrc S{};
   S.kres = static_cast<const _Float16*>(k_res);
   S.vres = static_cast<const _Float16*>(v_res);
-  S.res_rows = residual;
+  S.res_rows = res_rows;
   S.sinkq = QRegion{u8(0), f16(1), f16(2), u8(3), f16(4), f16(5)};
   if (win_tok > 0)
     S.winq = QRegion{u8(6), f16(7), f16(8), u8(9), f16(10), f16(11)};

@@ -153,14 +153,15 @@ def sparse_decode_attention_quantized(
 ):
     """k_cache/v_cache here is the RESIDUAL cache specifically (own
     [.., RESIDUAL_SIZE, D_HEAD] shape) -- not the full compacted cache like
-    sparse_decode_attention takes. Assumes WINDOW >= RESIDUAL_SIZE
-    (see build_quantized_kv_cache).
+    sparse_decode_attention takes.
 
     Mirrors quant_kernel.py:551-581.  Slot s of the logical [sink + window]
     cache is the sink token s (s < sink), the window-old token s - sink, or
     the residual row s - (sink + window - residual_size); slots are attended
-    under the _kv_indices validity rule.  window < residual_size raises
-    ValueError (the reference leaves it undefined).
+    under the _kv_indices validity rule.  window < residual_size, which the
+    reference leaves undefined (quant_kernel.py:589-590), means the whole
+    window stays fp16: k_cache / v_cache are [.., window, D_HEAD] (what
+    build_quantized_kv_cache returns then) and there is no window-old part.
     """
     tensors = dict(zip(_KIVI_ORDER, (k_sink_packed, k_sink_scale, k_sink_zero,
                                      v_sink_packed, v_sink_scale, v_sink_zero,
@@ -172,12 +173,13 @@ def sparse_decode_attention_quantized(
     B, H, D = q.shape
     KVH = k_cache.shape[1]
     window, sink, seq_len, R = int(window), int(sink), int(seq_len), int(residual_size)
-    if window < R:
-        raise ValueError(f"window ({window}) < residual_size ({R}) is not supported")
-    win_tok = window - R
+    if window < 1:
+        raise ValueError(f"window ({window}) must be >= 1")
+    res_rows = min(window, R)
+    win_tok = window - res_rows
     G = group_size
-    _checks.require_shape("k_cache", k_cache, (B, KVH, R, D))
-    _checks.require_shape("v_cache", v_cache, (B, KVH, R, D))
+    _checks.require_shape("k_cache", k_cache, (B, KVH, res_rows, D))
+    _checks.require_shape("v_cache", v_cache, (B, KVH, res_rows, D))
     expect = {
         "k_sink_packed": (B, KVH, G // 4, D), "k_sink_scale": (B, KVH, 1, D), "k_sink_zero": (B, KVH, 1, D),
         "v_sink_packed": (B, KVH, G, D // 4), "v_sink_scale": (B, KVH, G, D // G),
@@ -213,10 +215,15 @@ def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=RESIDUAL_SI
     Mirrors quant_kernel.py:584-622 (same slicing, sink padded to one group by
     repeating token 0, same 14 keys).  The quantizers read the fp16 slices
     directly instead of ``.float()`` copies: fp16 -> fp32 is exact, so the
-    codes are identical.  Assumes WINDOW >= RESIDUAL_SIZE.
+    codes are identical.  A window shorter than residual_size (undefined in
+    the reference, whose slicing would then put sink slots into the
+    residual) keeps the whole window as the fp16 residual and has no
+    window-old part.
     """
-    k_residual = k_compacted[:, :, -residual_size:, :].contiguous()
-    v_residual = v_compacted[:, :, -residual_size:, :].contiguous()
+    n = k_compacted.shape[2]
+    residual_size = min(residual_size, n - sink)
+    k_residual = k_compacted[:, :, n - residual_size:, :].contiguous()
+    v_residual = v_compacted[:, :, n - residual_size:, :].contiguous()
 
     k_sink_real = k_compacted[:, :, :sink, :]
     v_sink_real = v_compacted[:, :, :sink, :]
@@ -224,7 +231,6 @@ def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=RESIDUAL_SI
     k_sink_padded = torch.cat([k_sink_real, k_sink_real[:, :, :1, :].expand(-1, -1, pad, -1)], dim=2).contiguous()
     v_sink_padded = torch.cat([v_sink_real, v_sink_real[:, :, :1, :].expand(-1, -1, pad, -1)], dim=2).contiguous()
 
-    n = k_compacted.shape[2]
     k_window_old = k_compacted[:, :, sink:n - residual_size, :].contiguous()
     v_window_old = v_compacted[:, :, sink:n - residual_size, :].contiguous()
 

@@ -350,10 +350,13 @@ def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=128, sink=4
     (kept in the input dtype); sink = the ``sink`` real tokens padded to one
     group by repeating token 0, quantized; window-old = slots
     [sink, sink + W - residual), quantized.  Returns the 14-key dict.
+    A window W < residual (undefined in the reference) keeps the whole
+    window as the residual and has no window-old part (this build's rule).
     """
     k_compacted = np.asarray(k_compacted)
     v_compacted = np.asarray(v_compacted)
     n = k_compacted.shape[2]
+    residual_size = min(residual_size, n - sink)
     kres = np.ascontiguousarray(k_compacted[:, :, n - residual_size:])
     vres = np.ascontiguousarray(v_compacted[:, :, n - residual_size:])
     pad = group_size - sink
@@ -445,7 +448,7 @@ def quantized_attention_masked(q, cache, seq_len, window, sm_scale, sink=4, resi
     kv_indices marks valid (quant_kernel.py:485,496).  Equals
     ``quantized_attention`` in steady state.
     """
-    k, v = dequantized_regimes(cache, window - residual_size, sink, group_size)
+    k, v = dequantized_regimes(cache, max(window - residual_size, 0), sink, group_size)
     valid = slot_validity(seq_len, window, sink, 0)
     return masked_attention(q, k, v, valid, sm_scale, dtype)
 

@@ -147,7 +147,7 @@ def test_kivi_validation():
     assert _kivi(ptrs=[0x1000] * 6 + [None] * 6) == E["NULL"]          # window-old needed at W=256
     assert _kivi(bits=4) == E["BITS"]
     assert _kivi(group=64) == E["UNSUPPORTED"]
-    assert _kivi(W=64) == E["WINDOW"]                                 # W < residual
+    assert _kivi(W=0) == E["WINDOW"]                                  # empty window
     assert _kivi(S=0) == E["WINDOW"]
     assert _kivi(S=33) == E["WINDOW"]
     assert _kivi(R=100) == E["WINDOW"]

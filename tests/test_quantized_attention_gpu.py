@@ -132,6 +132,33 @@ def test_quantized_attention_rampup(L, device):
     assert max_abs(o, ref) < ATTN_TOL
 
 
+@pytest.mark.parametrize("W", [32, 48, 96])
+@pytest.mark.parametrize("L", [20, 163840])
+def test_quantized_attention_window_below_residual(W, L, device):
+    """window < residual_size (config 5's W=32; undefined in the reference):
+    the whole window stays fp16, the sink is quantized.  Steady state and
+    ramp-up (seq_len 20: the window's first slots are unwritten)."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D = 4, 32, 4, 128
+    if L >= S + W:                                   # steady state: every slot written
+        kc = randn((B, KVH, S + W, D), 50 + W)
+        vc = randn((B, KVH, S + W, D), 51 + W)
+    else:
+        kc, vc = O.build_compacted_cache(randn((B, KVH, L, D), 50 + W), randn((B, KVH, L, D), 51 + W),
+                                         L, W, S, garbage=3.0)
+    q16 = randn((B, H, D), 52 + W, np.float16)
+    say(f"kivi W={W} < R, L={L}")
+    cache = build_quantized_kv_cache(dev(kc.astype(np.float16), device), dev(vc.astype(np.float16), device))
+    hc = _host_cache(cache)
+    assert hc["k_residual"].shape[2] == W and hc["k_win_packed"].shape[2] == 0
+    oc = O.build_quantized_kv_cache(kc.astype(np.float16), vc.astype(np.float16))
+    for key in O.CACHE_KEYS:
+        np.testing.assert_array_equal(hc[key], oc[key], err_msg=key)
+    o = _attend(dev(q16, device), cache, L, W)
+    ref = O.quantized_attention_masked(q16, hc, L, W, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+
+
 def test_quantized_attention_rejects_small_window(device):
     from quant_kernel import build_quantized_kv_cache
     kc = torch.zeros(1, 2, S + 256, 128, dtype=torch.float16, device=device)
