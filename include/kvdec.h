@@ -195,6 +195,29 @@ int kvdec_kivi_stream_decode(const void* q, const void* k_ring,
                              void* stream);
 
 /*
+ * The whole KIVI cache from a compacted K/V cache in one launch.  Replaces
+ * build_quantized_kv_cache (quant_kernel.py:584-622: slicing :592-593 and
+ * :608-609, sink padding :602-606, four quantizer calls :611-614).
+ *   k_compacted, v_compacted : [B, KVH, n_slots, D] of in_dtype (KVDEC_F32,
+ *     KVDEC_F16 or KVDEC_BF16), n_slots = sink + window.
+ *   out[14], in the reference dict's key order: k_residual, v_residual
+ *     [B, KVH, min(window, residual), D] of residual_dtype (in_dtype, or
+ *     KVDEC_F16 for kvdec_sparse_decode_kivi); then the twelve tensors of
+ *     kvdec_sparse_decode_kivi's kivi[12] (sink group: the sink tokens, then
+ *     token 0 repeated up to `group` tokens; window-old: slots
+ *     [sink, sink + window - residual)).  The six window-old pointers may be
+ *     NULL when window <= residual.
+ *   Codes, scales and zeros equal kvdec_quantize_k / kvdec_quantize_v on the
+ *   same slices.  (window - residual) % group == 0 when window > residual;
+ *   1 <= sink <= group; D % group == 0; group == 32, bits == 2.
+ */
+int kvdec_build_kivi_cache(const void* k_compacted, const void* v_compacted,
+                           int in_dtype, int residual_dtype, int64_t B,
+                           int32_t KVH, int32_t n_slots, int32_t D,
+                           int32_t sink, int32_t residual, int32_t group,
+                           int32_t bits, void* const* out, void* stream);
+
+/*
  * Dequantize one block_n-token tile of a K region, with the reference's
  * clamping: byte = clamp(tok_start/4 + t/4, 0, num_packed-1) (C division),
  * code = (byte >> 2*(t%4)) & 3, group = min(byte/(group/4), num_groups-1),

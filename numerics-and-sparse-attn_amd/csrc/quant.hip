@@ -134,6 +134,34 @@ __device__ __forceinline__ uint32_t put_code(float c, uint32_t b, uint32_t w) {
   return __builtin_amdgcn_cvt_pk_u8_f32(c, b, w);
 }
 
+// One 32-value group (x in group order) quantized by one thread: byte b of
+// the result holds the codes of x[4b .. 4b+3], LSB first (the K and V
+// packings differ only in where those 8 bytes go).
+__device__ __forceinline__ u32x2 quant_group(const float (&x)[32], QParams& q) {
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int i = 1; i < 32; ++i) {
+    mn = fminf(mn, x[i]);
+    mx = fmaxf(mx, x[i]);
+  }
+  q = make_params(mn, mx);
+  u32x2 out;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float c = q.fast ? quant_code<true>(x[16 * w + 4 * b + j], q)
+                               : quant_code<false>(x[16 * w + 4 * b + j], q);
+        word |= (uint32_t)c << (8 * b + 2 * j);
+      }
+    out[w] = word;
+  }
+  return out;
+}
+
 // K: one lane owns two adjacent channels of one 32-token group; a wave owns
 // a 128-channel slice.  unit = pg * chunks + chunk with pg = pair * groups +
 // grp, the group's index over all (b, kv) heads: its input rows start at row
@@ -449,60 +477,118 @@ __global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
     }
   if (a.blk < 0) return;
   const size_t blk0 = (size_t)pair * a.cap + (size_t)a.blk * kGroup;   // first ring row of the block
+  const size_t g = (size_t)pair * a.nwg + a.slot;
   // K: one thread per channel, its 32 tokens (per-channel group)
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float x[kGroup];
 #pragma unroll
     for (int t = 0; t < kGroup; ++t) x[t] = (float)a.k_ring[(blk0 + t) * D + d];
-    float mn = x[0], mx = x[0];
+    QParams q;
+    const u32x2 c = quant_group(x, q);
 #pragma unroll
-    for (int t = 1; t < kGroup; ++t) {
-      mn = fminf(mn, x[t]);
-      mx = fmaxf(mx, x[t]);
-    }
-    const QParams q = make_params(mn, mx);
-    const size_t g = (size_t)pair * a.nwg + a.slot;
-#pragma unroll
-    for (int p = 0; p < kGroup / 4; ++p) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float c = q.fast ? quant_code<true>(x[4 * p + j], q) : quant_code<false>(x[4 * p + j], q);
-        w |= (uint32_t)c << (2 * j);
-      }
-      a.kp[(g * (kGroup / 4) + p) * D + d] = (uint8_t)w;
-    }
+    for (int p = 0; p < kGroup / 4; ++p) a.kp[(g * (kGroup / 4) + p) * D + d] = (uint8_t)(c[p >> 2] >> (8 * (p & 3)));
     a.ks[g * D + d] = (_Float16)q.s;
     a.kz[g * D + d] = (_Float16)q.z;
   }
   // V: one thread per (token, 32-channel group)
   const int ng = D / kGroup;
   for (int u = threadIdx.x; u < kGroup * ng; u += blockDim.x) {
-    const int t = u / ng, c = u % ng;
-    const _Float16* src = a.v_ring + (blk0 + t) * D + c * kGroup;
+    const int t = u / ng, cg = u % ng;
+    const _Float16* src = a.v_ring + (blk0 + t) * D + cg * kGroup;
     float x[kGroup];
 #pragma unroll
     for (int i = 0; i < kGroup; ++i) x[i] = (float)src[i];
-    float mn = x[0], mx = x[0];
-#pragma unroll
-    for (int i = 1; i < kGroup; ++i) {
-      mn = fminf(mn, x[i]);
-      mx = fmaxf(mx, x[i]);
+    QParams q;
+    const u32x2 c = quant_group(x, q);
+    const size_t tok = g * kGroup + t;
+    *reinterpret_cast<u32x2*>(a.vp + tok * (D / 4) + cg * (kGroup / 4)) = c;
+    a.vs[tok * ng + cg] = (_Float16)q.s;
+    a.vz[tok * ng + cg] = (_Float16)q.z;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The whole KIVI cache from a compacted [B, KVH, sink + window, D] cache in
+// one launch (the reference's build_quantized_kv_cache, quant_kernel.py:584-
+// 622): residual rows copied (input dtype, or fp16 for the decode), the sink
+// group (sink real tokens, the rest token 0 again) and the window-old groups
+// quantized.  Grid: x = (b, kv) head, y = slices of that head's work.
+// ---------------------------------------------------------------------------
+struct BuildArgs {
+  const void* kc;
+  const void* vc;
+  int n, D, sink, res_rows, win_tok;
+  void* kres;
+  void* vres;
+  uint8_t* kp[2];   // [0] sink, [1] window-old
+  _Float16* ks[2];
+  _Float16* kz[2];
+  uint8_t* vp[2];
+  _Float16* vs[2];
+  _Float16* vz[2];
+};
+
+template <typename T>
+__device__ __forceinline__ float elem(const void* p, size_t i) {
+  if constexpr (std::is_same<T, uint16_t>::value)
+    return __builtin_bit_cast(float, (uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
+  else
+    return (float)static_cast<const T*>(p)[i];
+}
+
+template <typename T, typename RT>
+__global__ __launch_bounds__(256) void build_kernel(BuildArgs a) {
+  const int64_t pair = blockIdx.x;
+  const int D = a.D, ng = D / kGroup, nwg = a.win_tok / kGroup;
+  const int first = blockIdx.y * blockDim.x + threadIdx.x, stride = gridDim.y * blockDim.x;
+  const size_t in0 = (size_t)pair * a.n * D;
+  // residual: the last res_rows slots (same element type, or fp16)
+  const size_t res0 = (size_t)(a.n - a.res_rows) * D;
+  for (int i = first; i < a.res_rows * D; i += stride) {
+    const size_t o = (size_t)pair * a.res_rows * D + i;
+    if constexpr (std::is_same<T, RT>::value) {
+      static_cast<T*>(a.kres)[o] = static_cast<const T*>(a.kc)[in0 + res0 + i];
+      static_cast<T*>(a.vres)[o] = static_cast<const T*>(a.vc)[in0 + res0 + i];
+    } else {
+      static_cast<RT*>(a.kres)[o] = (RT)elem<T>(a.kc, in0 + res0 + i);
+      static_cast<RT*>(a.vres)[o] = (RT)elem<T>(a.vc, in0 + res0 + i);
     }
-    const QParams q = make_params(mn, mx);
-    const size_t tok = ((size_t)pair * a.nwg + a.slot) * kGroup + t;
+  }
+  // K groups: region 0 = the sink group (slot t, or slot 0 past the sink
+  // tokens), region 1 = window-old group g (slots sink + 32 g + t)
+  for (int task = first; task < (1 + nwg) * D; task += stride) {
+    const int grp = task / D, d = task % D;   // grp 0: sink
+    const int r = grp == 0 ? 0 : 1, g = grp - r;
+    float x[kGroup];
 #pragma unroll
-    for (int b = 0; b < kGroup / 4; ++b) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float cc = q.fast ? quant_code<true>(x[4 * b + j], q) : quant_code<false>(x[4 * b + j], q);
-        w |= (uint32_t)cc << (2 * j);
-      }
-      a.vp[tok * (D / 4) + c * (kGroup / 4) + b] = (uint8_t)w;
+    for (int t = 0; t < kGroup; ++t) {
+      const int slot = r == 0 ? (t < a.sink ? t : 0) : a.sink + kGroup * g + t;
+      x[t] = elem<T>(a.kc, in0 + (size_t)slot * D + d);
     }
-    a.vs[tok * ng + c] = (_Float16)q.s;
-    a.vz[tok * ng + c] = (_Float16)q.z;
+    QParams q;
+    const u32x2 c = quant_group(x, q);
+    const size_t gi = (size_t)pair * (r == 0 ? 1 : nwg) + g;
+#pragma unroll
+    for (int p = 0; p < kGroup / 4; ++p)
+      a.kp[r][(gi * (kGroup / 4) + p) * D + d] = (uint8_t)(c[p >> 2] >> (8 * (p & 3)));
+    a.ks[r][gi * D + d] = (_Float16)q.s;
+    a.kz[r][gi * D + d] = (_Float16)q.z;
+  }
+  // V: one task per (token, 32-channel group); tokens 0..31 of the sink
+  // group, then the window-old tokens
+  for (int task = first; task < (kGroup + a.win_tok) * ng; task += stride) {
+    const int tk = task / ng, cg = task % ng;
+    const int r = tk < kGroup ? 0 : 1, t = tk - (r ? kGroup : 0);
+    const int slot = r == 0 ? (t < a.sink ? t : 0) : a.sink + t;
+    float x[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) x[i] = elem<T>(a.vc, in0 + (size_t)slot * D + cg * kGroup + i);
+    QParams q;
+    const u32x2 c = quant_group(x, q);
+    const size_t tok = (size_t)pair * (r == 0 ? kGroup : a.win_tok) + t;
+    *reinterpret_cast<u32x2*>(a.vp[r] + tok * (D / 4) + cg * (kGroup / 4)) = c;
+    a.vs[r][tok * ng + cg] = (_Float16)q.s;
+    a.vz[r][tok * ng + cg] = (_Float16)q.z;
   }
 }
 
@@ -634,6 +720,62 @@ int kvdec_kivi_stream_append(const void* k_new, const void* v_new, void* k_ring,
   }
   hipLaunchKernelGGL(stream_append_kernel, dim3((unsigned)(B * KVH)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
+  return launch_status();
+}
+
+int kvdec_build_kivi_cache(const void* k_compacted, const void* v_compacted, int in_dtype,
+                           int residual_dtype, int64_t B, int32_t KVH, int32_t n_slots, int32_t D, int32_t sink,
+                           int32_t residual, int32_t group, int32_t bits, void* const* out,
+                           void* stream) {
+  if (!k_compacted || !v_compacted || !out) return KVDEC_E_NULL;
+  if (bits != 2) return KVDEC_E_BITS;
+  if (group != kGroup) return KVDEC_E_UNSUPPORTED;
+  if (in_dtype != KVDEC_F32 && in_dtype != KVDEC_F16 && in_dtype != KVDEC_BF16) return KVDEC_E_DTYPE;
+  if (residual_dtype != in_dtype && residual_dtype != KVDEC_F16) return KVDEC_E_DTYPE;
+  if (B < 1 || KVH < 1 || D < 1 || B * (int64_t)KVH > 0x7fffffffLL) return KVDEC_E_SHAPE;
+  if (D % kGroup != 0) return KVDEC_E_DGROUP;
+  if (sink < 1 || sink > kGroup || residual < 1 || n_slots <= sink) return KVDEC_E_WINDOW;
+  if ((int64_t)n_slots * D > 0x7fffffffLL) return KVDEC_E_SHAPE;
+  const int window = n_slots - sink;
+  const int res_rows = window < residual ? window : residual;
+  const int win_tok = window - res_rows;
+  if (win_tok % kGroup != 0) return KVDEC_E_GROUP;
+  for (int i = 0; i < 8; ++i)
+    if (!out[i]) return KVDEC_E_NULL;
+  if (win_tok > 0)
+    for (int i = 8; i < 14; ++i)
+      if (!out[i]) return KVDEC_E_NULL;
+  BuildArgs a{};
+  a.kc = k_compacted;
+  a.vc = v_compacted;
+  a.n = n_slots;
+  a.D = D;
+  a.sink = sink;
+  a.res_rows = res_rows;
+  a.win_tok = win_tok;
+  a.kres = out[0];
+  a.vres = out[1];
+  for (int r = 0; r < 2; ++r) {
+    if (r == 1 && win_tok == 0) break;
+    a.kp[r] = static_cast<uint8_t*>(out[2 + 6 * r]);
+    a.ks[r] = static_cast<_Float16*>(out[3 + 6 * r]);
+    a.kz[r] = static_cast<_Float16*>(out[4 + 6 * r]);
+    a.vp[r] = static_cast<uint8_t*>(out[5 + 6 * r]);
+    a.vs[r] = static_cast<_Float16*>(out[6 + 6 * r]);
+    a.vz[r] = static_cast<_Float16*>(out[7 + 6 * r]);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // about 1024 work items per workgroup, at most 64 workgroups per head
+  const int64_t items = std::max<int64_t>((int64_t)res_rows * D, (int64_t)(kGroup + win_tok) * (D / kGroup));
+  const unsigned split = (unsigned)std::min<int64_t>(64, std::max<int64_t>(1, (items + 1023) / 1024));
+  const dim3 grid((unsigned)(B * KVH), split);
+  const bool same = residual_dtype == in_dtype;
+  void (*kern)(BuildArgs) = build_kernel<_Float16, _Float16>;
+  if (in_dtype == KVDEC_F32)
+    kern = same ? build_kernel<float, float> : build_kernel<float, _Float16>;
+  else if (in_dtype == KVDEC_BF16)
+    kern = same ? build_kernel<uint16_t, uint16_t> : build_kernel<uint16_t, _Float16>;
+  hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, a);
   return launch_status();
 }
 

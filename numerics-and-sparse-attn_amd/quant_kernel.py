@@ -207,42 +207,67 @@ def sparse_decode_attention_quantized(
     return o
 
 
-def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=RESIDUAL_SIZE, sink=SINK_SIZE):
+def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=RESIDUAL_SIZE, sink=SINK_SIZE,
+                             residual_dtype=None):
     """Slices a compacted [BATCH, N_KV_HEADS, SINK+WINDOW, D_HEAD] K/V cache
     into residual/sink/window-old and quantizes sink+window-old separately,
     producing the tensors sparse_decode_attention_quantized expects.
 
     Mirrors quant_kernel.py:584-622 (same slicing, sink padded to one group by
-    repeating token 0, same 14 keys).  The quantizers read the fp16 slices
-    directly instead of ``.float()`` copies: fp16 -> fp32 is exact, so the
-    codes are identical.  A window shorter than residual_size (undefined in
-    the reference, whose slicing would then put sink slots into the
-    residual) keeps the whole window as the fp16 residual and has no
+    repeating token 0, same 14 keys) in one kernel launch that reads the
+    compacted cache once: no slice, pad or ``.float()`` copies (fp16 / bf16
+    -> fp32 is exact, so the codes equal the quantizers' on those copies).
+    The residual keeps the input dtype, as in the reference, unless
+    residual_dtype says otherwise (torch.float16 turns an fp32 or bf16 cache
+    into what the fused decode reads).  A window shorter than residual_size
+    (undefined in the reference, whose slicing would then put sink slots into
+    the residual) keeps the whole window as the residual and has no
     window-old part.
     """
-    n = k_compacted.shape[2]
-    residual_size = min(residual_size, n - sink)
-    k_residual = k_compacted[:, :, n - residual_size:, :].contiguous()
-    v_residual = v_compacted[:, :, n - residual_size:, :].contiguous()
+    _checks.require_gpu_tensor("k_compacted", k_compacted, dtypes=tuple(_IN_DTYPES), ndim=4,
+                               contiguous=False)
+    _checks.require_gpu_tensor("v_compacted", v_compacted, dtypes=tuple(_IN_DTYPES), ndim=4,
+                               contiguous=False)
+    B, KVH, n, D = k_compacted.shape
+    _checks.require_same_device(("k_compacted", k_compacted), ("v_compacted", v_compacted))
+    _checks.require_shape("v_compacted", v_compacted, (B, KVH, n, D))
+    if v_compacted.dtype != k_compacted.dtype:
+        raise TypeError(f"v_compacted dtype {v_compacted.dtype} != k_compacted dtype {k_compacted.dtype}")
+    sink = int(sink)
+    if not 1 <= sink <= GROUP_SIZE or n <= sink:
+        raise ValueError(f"unsupported sink={sink} for a cache of {n} slots")
+    res_dtype = k_compacted.dtype if residual_dtype is None else residual_dtype
+    if res_dtype not in (k_compacted.dtype, torch.float16):
+        raise TypeError(f"residual_dtype must be the input dtype or torch.float16, got {res_dtype}")
+    res = min(int(residual_size), n - sink)
+    win = n - sink - res
+    if win % GROUP_SIZE != 0:
+        raise AssertionError("this simple version assumes seq_len is a multiple of group_size")
+    k_compacted = k_compacted.contiguous()
+    v_compacted = v_compacted.contiguous()
+    dev, G, P = k_compacted.device, GROUP_SIZE, 8 // QUANT_BITS
 
-    k_sink_real = k_compacted[:, :, :sink, :]
-    v_sink_real = v_compacted[:, :, :sink, :]
-    pad = GROUP_SIZE - sink
-    k_sink_padded = torch.cat([k_sink_real, k_sink_real[:, :, :1, :].expand(-1, -1, pad, -1)], dim=2).contiguous()
-    v_sink_padded = torch.cat([v_sink_real, v_sink_real[:, :, :1, :].expand(-1, -1, pad, -1)], dim=2).contiguous()
+    def u8(*shape):
+        return torch.empty(shape, dtype=torch.uint8, device=dev)
 
-    k_window_old = k_compacted[:, :, sink:n - residual_size, :].contiguous()
-    v_window_old = v_compacted[:, :, sink:n - residual_size, :].contiguous()
+    def f16(*shape):
+        return torch.empty(shape, dtype=torch.float16, device=dev)
 
-    k_sink_packed, k_sink_scale, k_sink_zero = quantize_k_cache(k_sink_padded)
-    v_sink_packed, v_sink_scale, v_sink_zero = quantize_v_cache(v_sink_padded)
-    k_win_packed, k_win_scale, k_win_zero = quantize_k_cache(k_window_old)
-    v_win_packed, v_win_scale, v_win_zero = quantize_v_cache(v_window_old)
-
-    return {
-        "k_residual": k_residual, "v_residual": v_residual,
-        "k_sink_packed": k_sink_packed, "k_sink_scale": k_sink_scale, "k_sink_zero": k_sink_zero,
-        "v_sink_packed": v_sink_packed, "v_sink_scale": v_sink_scale, "v_sink_zero": v_sink_zero,
-        "k_win_packed": k_win_packed, "k_win_scale": k_win_scale, "k_win_zero": k_win_zero,
-        "v_win_packed": v_win_packed, "v_win_scale": v_win_scale, "v_win_zero": v_win_zero,
+    out = {
+        "k_residual": torch.empty((B, KVH, res, D), dtype=res_dtype, device=dev),
+        "v_residual": torch.empty((B, KVH, res, D), dtype=res_dtype, device=dev),
+        "k_sink_packed": u8(B, KVH, G // P, D), "k_sink_scale": f16(B, KVH, 1, D),
+        "k_sink_zero": f16(B, KVH, 1, D),
+        "v_sink_packed": u8(B, KVH, G, D // P), "v_sink_scale": f16(B, KVH, G, D // G),
+        "v_sink_zero": f16(B, KVH, G, D // G),
+        "k_win_packed": u8(B, KVH, win // P, D), "k_win_scale": f16(B, KVH, win // G, D),
+        "k_win_zero": f16(B, KVH, win // G, D),
+        "v_win_packed": u8(B, KVH, win, D // P), "v_win_scale": f16(B, KVH, win, D // G),
+        "v_win_zero": f16(B, KVH, win, D // G),
     }
+    ptrs = (K._vp * 14)(*[K.ptr(t) if t.numel() else None for t in out.values()])
+    rc = K.lib.kvdec_build_kivi_cache(K.ptr(k_compacted), K.ptr(v_compacted), _IN_DTYPES[k_compacted.dtype],
+                                      _IN_DTYPES[res_dtype], B, KVH, n, D, sink, int(residual_size), G,
+                                      QUANT_BITS, ptrs, K.stream_of(k_compacted))
+    K.check(rc, "build_quantized_kv_cache")
+    return out

@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 13
+    assert len(funcs) == 14
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -225,6 +225,32 @@ def test_stream_decode_validation():
     assert _sdecode(count=0) == E["WINDOW"]
     assert _sdecode(count=161) == E["WINDOW"]
     assert _sdecode(KVH=3) == E["SHAPE"]
+
+
+def _build(**kw):
+    a = dict(k=FAKE, v=FAKE, dt=K.F16, rdt=K.F16, B=2, KVH=8, n=4 + 256, D=128, S=4, R=128, group=32,
+             bits=2, out=[0x1000] * 14, stream=None)
+    a.update(kw)
+    arr = (K._vp * 14)(*a["out"]) if a["out"] is not None else None
+    return K.lib.kvdec_build_kivi_cache(a["k"], a["v"], a["dt"], a["rdt"], a["B"], a["KVH"], a["n"],
+                                        a["D"], a["S"], a["R"], a["group"], a["bits"], arr, a["stream"])
+
+
+def test_build_cache_validation():
+    assert _build(k=None) == E["NULL"]
+    assert _build(out=None) == E["NULL"]
+    assert _build(out=[0x1000] * 13 + [None]) == E["NULL"]
+    assert _build(out=[0x1000] * 8 + [None] * 6) == E["NULL"]   # window-old part needed
+    assert _build(bits=4) == E["BITS"]
+    assert _build(group=64) == E["UNSUPPORTED"]
+    assert _build(dt=7) == E["DTYPE"]
+    assert _build(dt=K.F32, rdt=K.BF16) == E["DTYPE"]
+    assert _build(D=100) == E["DGROUP"]
+    assert _build(S=0) == E["WINDOW"]
+    assert _build(S=33) == E["WINDOW"]
+    assert _build(n=4) == E["WINDOW"]
+    assert _build(n=4 + 144) == E["GROUP"]
+    assert _build(B=0) == E["SHAPE"]
 
 
 def test_dequant_tile_validation():
