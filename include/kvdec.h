@@ -100,6 +100,43 @@ int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
                         size_t ws_bytes, void* stream);
 
 /*
+ * Dense decode over a paged or strided fp16 cache with per-sequence lengths
+ * (no counterpart in the reference, which passes one scalar seq_len and a
+ * contiguous cache: dense_kernel.py:70-82; this is the vLLM-style caller's
+ * form of the same attention).  Token t of sequence b, KV head h is the row
+ *   k_pages + page * page_stride + h * head_stride + (t % page_size) * row_stride
+ * (strides in elements; the last dim, D = 128, contiguous) with page =
+ * block_table[b * max_blocks + t / page_size].  block_table NULL: no paging,
+ * page = b (page_stride is the per-sequence stride) -- e.g. a [B, L, KVH, D]
+ * cache, or a [B, KVH, L_max, D] cache with per-sequence lengths.
+ * seq_lens [B] int32 on the device (NULL: every sequence max_seq_len long);
+ * lengths are clamped into [0, max_seq_len], a length of 0 gives zeros.
+ * page_size is a power of two >= 16 and max_blocks * page_size >=
+ * max_seq_len; page ids outside [0, num_pages) read as zeros.  ws /
+ * ws_bytes as for kvdec_dense_decode with L = max_seq_len
+ * (kvdec_workspace_bytes(KVDEC_KIND_DENSE, B, H, KVH, max_seq_len, D)).
+ */
+int kvdec_paged_decode(const void* q, const void* k_pages, const void* v_pages,
+                       const int32_t* block_table, const int32_t* seq_lens, void* o,
+                       int dtype, int64_t B, int32_t H, int32_t KVH, int32_t D,
+                       int64_t max_seq_len, int32_t page_size, int32_t max_blocks,
+                       int64_t num_pages, int64_t page_stride, int64_t row_stride,
+                       int64_t head_stride, float sm_scale, void* ws, size_t ws_bytes,
+                       void* stream);
+
+/*
+ * kvdec_sparse_decode with one seq_len per sequence (seq_lens [B] int32 on
+ * the device, each >= 1; the reference passes one scalar,
+ * sparse_kernel.py:105-118).  Same cache, layouts, masking rule per
+ * sequence and workspace (kvdec_workspace_bytes(KVDEC_KIND_SPARSE, ...)).
+ */
+int kvdec_sparse_decode_varlen(const void* q, const void* k_cache, const void* v_cache,
+                               void* o, const int32_t* seq_lens, int dtype, int64_t B,
+                               int32_t H, int32_t KVH, int32_t window, int32_t sink,
+                               int32_t layout, float sm_scale, void* ws, size_t ws_bytes,
+                               void* stream);
+
+/*
  * KIVI per-channel quantization of K.  Replaces quant_kernel.py:106-126
  * (quantize_k_cache) and quant_kernel.py:44-103.
  *   x      : [B, KVH, N, D] of in_dtype (KVDEC_F32, KVDEC_F16 or KVDEC_BF16)

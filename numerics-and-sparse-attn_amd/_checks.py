@@ -29,3 +29,17 @@ def require_same_device(*named) -> None:
     if len(devs) > 1:
         raise ValueError("all tensors must be on the same device: "
                          + ", ".join(f"{n}={t.device}" for n, t in named if t is not None))
+
+
+def seq_lens_tensor(name: str, t, B: int, device) -> None:
+    """Per-sequence lengths: a [B] int32 tensor on the cache's device."""
+    require_gpu_tensor(name, t, dtypes=(torch.int32,), ndim=1)
+    require_shape(name, t, (B,))
+    if t.device != device:
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+
+
+def row_major_rows(name: str, t) -> None:
+    """The head dim (last) must be contiguous; other strides are free."""
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} must have a contiguous last dimension, got strides {t.stride()}")

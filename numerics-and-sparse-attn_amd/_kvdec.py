@@ -41,6 +41,11 @@ SIGNATURES = {
                                           _i32, _f32, _vp, _sz, _vp]),
     "kvdec_sparse_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32, _i64,
                                            _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
+    "kvdec_paged_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32,
+                                          _i32, _i64, _i32, _i32, _i64, _i64, _i64, _i64, _f32, _vp,
+                                          _sz, _vp]),
+    "kvdec_sparse_decode_varlen": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32,
+                                                  _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
     "kvdec_quantize_k": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _vp, _vp, _i64, _i32, _i64, _i32,
                                         _i32, _i32, _vp]),
     "kvdec_quantize_v": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _vp, _vp, _i64, _i32, _i64, _i32,

@@ -279,7 +279,7 @@ __device__ __forceinline__ void merge_out(const AttnCommon& P, char* lds, int64_
     acc += ow[w] * f;
   }
   if (P.n_splits == 1) {
-    const float inv = 1.0f / L;
+    const float inv = L > 0.f ? 1.0f / L : 0.f;   // L == 0: a sequence of length 0
     half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
                 (_Float16)(acc[3] * inv)};
     *reinterpret_cast<half4v*>(P.o + ((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim +
@@ -292,6 +292,28 @@ __device__ __forceinline__ void merge_out(const AttnCommon& P, char* lds, int64_
       P.ws[total * kHeadDim + total + idx] = L;
     }
   }
+}
+
+// Validity ranges of the [sink + window] cache at this length (the
+// _kv_indices rule for the linear layout), clamped into [0, sink + window].
+__host__ __device__ inline SlotRanges sparse_ranges(int64_t seq_len, int32_t window, int32_t sink,
+                                                   int32_t layout) {
+  const int64_t S = sink, W = window, n = S + W;
+  auto clamp = [n](int64_t v) { return (int)(v < 0 ? 0 : (v > n ? n : v)); };
+  SlotRanges R;
+  R.va = clamp(seq_len < S ? seq_len : S);
+  if (layout == KVDEC_LAYOUT_LINEAR) {
+    const int64_t lo = 2 * S + W - seq_len;
+    R.vb = clamp(lo > S ? lo : S);
+    R.vc = clamp(n);
+  } else {
+    int64_t nwin = seq_len - S;
+    if (nwin < 0) nwin = 0;
+    if (nwin > W) nwin = W;
+    R.vb = clamp(S);
+    R.vc = clamp(S + nwin);
+  }
+  return R;
 }
 
 // fp16 rows: the dense cache [B, KVH, L, 128] or the compacted sparse cache
@@ -321,6 +343,126 @@ struct F16Src {
     ring_begin(it, ring, wave, wave + kWaves, lane);
     StepCtx c;
     sync(c, it.n > 2 * kWaves);
+    if (it.n > 2 * kWaves)
+      ring_run_dynamic(it, ring, ctr, st, c);
+    else
+      ring_run_static(it, ring, st, c);
+    publish_ml(P, st, c.lds, lane, wave);
+    publish_f(P, st, c.slot, lane);
+  }
+};
+
+// A token-indexed fp16 cache with its own strides, optionally paged.  Token
+// t of sequence b, KV head h sits at
+//   base + page(b, t) * page_bytes + h * head_bytes + (t mod page_size) * row_bytes
+// with page(b, t) = block_table[b][t / page_size]; without a table the
+// "page" is the sequence (page(b, t) = b, page_size unbounded) holding
+// `rows` rows.  A 32-token tile is two 16-row halves; page sizes are powers
+// of two >= 16, so a half never straddles two pages, and each half gets a
+// buffer resource of its own that ends at the half's last row (page ids
+// outside [0, num_pages), rows past `rows` and halves with no valid token
+// load zeros without touching memory).
+typedef __attribute__((address_space(4))) const int32_t cint32;
+
+struct PagedItems {
+  typedef F16Raw Raw;
+  const char* kb;      // this KV head's origin (+ the sequence's when untabled)
+  const char* vb;
+  cint32* bt;          // this sequence's block-table row, or null
+  int64_t page_bytes;
+  uint32_t row_bytes;
+  int ps_log2, max_blocks;
+  int64_t num_pages;
+  int rows;            // untabled: rows of the sequence's region
+  int tile0, n;
+  SlotRanges R;
+
+  __device__ __forceinline__ void load(int i, Raw& X, int lane) const {
+    const int tile = tile0 + i;
+    const bool live = i < n;
+    rsrc_t rk[2], rv[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int tok = kTile * tile + 16 * h;
+      bool ok = live && (tok < R.va || (tok + 16 > R.vb && tok < R.vc));
+      int64_t off;
+      int nr = 16;         // rows of this half inside the page / region
+      if (bt) {
+        const int idx = min(tok >> ps_log2, max_blocks - 1);   // always inside the row
+        const int64_t page = bt[idx];
+        ok = ok && page >= 0 && page < num_pages;
+        off = page * page_bytes + (int64_t)(tok & ((1 << ps_log2) - 1)) * row_bytes;
+      } else {
+        off = (int64_t)tok * row_bytes;
+        nr = min(16, rows - tok);
+      }
+      const uint32_t bytes = ok && nr > 0 ? (uint32_t)(nr - 1) * row_bytes + kRowBytes : 0u;
+      rk[h] = make_rsrc(kb + off, bytes);
+      rv[h] = make_rsrc(vb + off, bytes);
+    }
+    // the rows of load_f16: K rows 4i + g (half i / 4), V rows tau(g, j)
+    // (half j / 4), at (row mod 16) * row_bytes inside the half
+    const uint32_t t = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      X.k[k] = bload16(rk[k >> 2], ((4u * k + g) & 15u) * row_bytes + 16u * t);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      X.v[j] = bload16(rv[j >> 2], (4u * g + (j & 3)) * row_bytes + 16u * t);
+  }
+  typedef WaveState State;
+  __device__ __forceinline__ void step(int i, const Raw& X, State& st, const StepCtx& c) const {
+    f16_tile_step(X, c.slot, c.qB, kTile * (tile0 + i), c.R, c.scale_log2, st, c.lane);
+  }
+};
+
+// Per-sequence lengths over a paged or strided cache: dense attention over
+// the first len(b) tokens, or (sparse) the sink + window rule over a
+// compacted [sink + window] cache at position len(b).
+struct PagedSrc {
+  const char* k;
+  const char* v;
+  const int32_t* bt;     // [B, max_blocks] or null
+  const int32_t* lens;   // [B] or null (every sequence max_len long)
+  int64_t page_bytes, head_bytes;
+  uint32_t row_bytes;
+  int ps_log2, max_blocks;
+  int64_t num_pages;
+  int max_len;           // dense: lengths are clamped into [0, max_len]
+  int rows;              // untabled: rows per (sequence, head) region
+  int window, sink, layout;
+  bool sparse;
+
+  __device__ __forceinline__ void init_counters(int* ctr) const { ctr[0] = 2 * kWaves; }
+
+  template <class Sync>
+  __device__ __forceinline__ void process(int64_t pair, int split, const AttnCommon& P, int wave,
+                                          int lane, int* ctr, Sync&& sync, WaveState& st) const {
+    const int64_t b = pair / P.KVH;
+    const int kvh = (int)(pair % P.KVH);
+    int len = max_len;
+    if (lens) len = min(max((int)((cint32*)lens)[b], 0), max_len);
+    const SlotRanges R = sparse ? sparse_ranges(len, window, sink, layout) : SlotRanges{len, 0, 0};
+    const int n_slots = sparse ? sink + window : len;
+    const int tiles = (n_slots + kTile - 1) / kTile;
+    PagedItems it;
+    it.kb = k + (int64_t)kvh * head_bytes + (bt ? 0 : b * page_bytes);
+    it.vb = v + (int64_t)kvh * head_bytes + (bt ? 0 : b * page_bytes);
+    it.bt = bt ? (cint32*)bt + b * max_blocks : nullptr;
+    it.page_bytes = page_bytes;
+    it.row_bytes = row_bytes;
+    it.rows = rows;
+    it.ps_log2 = ps_log2;
+    it.max_blocks = max_blocks;
+    it.num_pages = num_pages;
+    it.tile0 = split * P.tiles_per_split;
+    it.n = max(0, min(P.tiles_per_split, tiles - it.tile0));
+    it.R = R;
+    Ring<PagedItems> ring;
+    ring_begin(it, ring, wave, wave + kWaves, lane);
+    StepCtx c;
+    sync(c, it.n > 2 * kWaves);
+    c.R = R;
     if (it.n > 2 * kWaves)
       ring_run_dynamic(it, ring, ctr, st, c);
     else
@@ -543,7 +685,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnCommon P) {
     L += wl[idx] * f;
     acc += wo[idx * kHeadDim + d] * f;
   }
-  P.o[((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + d] = (_Float16)(acc / L);
+  P.o[((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + d] = (_Float16)(L > 0.f ? acc / L : 0.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -616,27 +758,6 @@ int launch_attn(AttnCommon P, const Src& S, bool kivi, size_t ws_bytes, hipStrea
   const int64_t outs = P.pairs * P.G * kHeadDim;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, stream, P);
   return launch_status();
-}
-
-// Validity ranges of the [sink + window] cache at this length (the
-// _kv_indices rule for the linear layout), clamped into [0, sink + window].
-SlotRanges sparse_ranges(int64_t seq_len, int32_t window, int32_t sink, int32_t layout) {
-  const int64_t S = sink, W = window, n = S + W;
-  auto clamp = [n](int64_t v) { return (int)(v < 0 ? 0 : (v > n ? n : v)); };
-  SlotRanges R;
-  R.va = clamp(seq_len < S ? seq_len : S);
-  if (layout == KVDEC_LAYOUT_LINEAR) {
-    const int64_t lo = 2 * S + W - seq_len;
-    R.vb = clamp(lo > S ? lo : S);
-    R.vc = clamp(n);
-  } else {
-    int64_t nwin = seq_len - S;
-    if (nwin < 0) nwin = 0;
-    if (nwin > W) nwin = W;
-    R.vb = clamp(S);
-    R.vc = clamp(S + nwin);
-  }
-  return R;
 }
 
 }  // namespace
@@ -728,6 +849,93 @@ int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
   P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
   P.R = sparse_ranges(seq_len, window, sink, layout);
   F16Src S{static_cast<const _Float16*>(k_cache), static_cast<const _Float16*>(v_cache), (int)n};
+  return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int kvdec_paged_decode(const void* q, const void* k_pages, const void* v_pages,
+                       const int32_t* block_table, const int32_t* seq_lens, void* o, int dtype,
+                       int64_t B, int32_t H, int32_t KVH, int32_t D, int64_t max_seq_len,
+                       int32_t page_size, int32_t max_blocks, int64_t num_pages,
+                       int64_t page_stride, int64_t row_stride, int64_t head_stride,
+                       float sm_scale, void* ws, size_t ws_bytes, void* stream) {
+  if (!q || !k_pages || !v_pages || !o) return KVDEC_E_NULL;
+  if (dtype != KVDEC_F16) return KVDEC_E_DTYPE;
+  int rc = check_heads(B, H, KVH, D);
+  if (rc) return rc;
+  if (max_seq_len < 1) return KVDEC_E_SEQLEN;
+  if (max_seq_len >= ((int64_t)1 << 30)) return KVDEC_E_SHAPE;
+  if (page_stride < 0 || row_stride < 0 || head_stride < 0) return KVDEC_E_SHAPE;
+  if (row_stride * 2 * 16 >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;   // 32-bit in-half offsets
+  int ps_log2 = 0;
+  if (block_table) {
+    if (page_size < 16 || page_size > (1 << 20) || (page_size & (page_size - 1))) return KVDEC_E_UNSUPPORTED;
+    while ((1 << ps_log2) < page_size) ++ps_log2;
+    if (num_pages < 1 || max_blocks < 1) return KVDEC_E_SHAPE;
+    if ((int64_t)max_blocks * page_size < max_seq_len) return KVDEC_E_SHAPE;
+  }
+  AttnCommon P{};
+  P.q = static_cast<const _Float16*>(q);
+  P.o = static_cast<_Float16*>(o);
+  P.ws = static_cast<float*>(ws);
+  P.pairs = B * KVH;
+  P.H = H;
+  P.KVH = KVH;
+  P.G = H / KVH;
+  P.n_tiles = (int)tiles_for(KVDEC_KIND_DENSE, max_seq_len);
+  P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
+  PagedSrc S{};
+  S.k = static_cast<const char*>(k_pages);
+  S.v = static_cast<const char*>(v_pages);
+  S.bt = block_table;
+  S.lens = seq_lens;
+  S.page_bytes = page_stride * 2;
+  S.head_bytes = head_stride * 2;
+  S.row_bytes = (uint32_t)(row_stride * 2);
+  S.ps_log2 = ps_log2;
+  S.max_blocks = max_blocks;
+  S.num_pages = num_pages;
+  S.max_len = (int)max_seq_len;
+  S.rows = (int)max_seq_len;
+  S.sparse = false;
+  return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int kvdec_sparse_decode_varlen(const void* q, const void* k_cache, const void* v_cache, void* o,
+                               const int32_t* seq_lens, int dtype, int64_t B, int32_t H,
+                               int32_t KVH, int32_t window, int32_t sink, int32_t layout,
+                               float sm_scale, void* ws, size_t ws_bytes, void* stream) {
+  if (!q || !k_cache || !v_cache || !o || !seq_lens) return KVDEC_E_NULL;
+  if (dtype != KVDEC_F16) return KVDEC_E_DTYPE;
+  int rc = check_heads(B, H, KVH, kHeadDim);
+  if (rc) return rc;
+  if (window < 0 || sink < 0 || (int64_t)window + sink < 1) return KVDEC_E_WINDOW;
+  if (layout != KVDEC_LAYOUT_LINEAR && layout != KVDEC_LAYOUT_RING) return KVDEC_E_UNSUPPORTED;
+  if (layout == KVDEC_LAYOUT_RING && window < 1) return KVDEC_E_WINDOW;
+  const int64_t n = (int64_t)window + sink;
+  if (n >= ((int64_t)1 << 30)) return KVDEC_E_SHAPE;
+  AttnCommon P{};
+  P.q = static_cast<const _Float16*>(q);
+  P.o = static_cast<_Float16*>(o);
+  P.ws = static_cast<float*>(ws);
+  P.pairs = B * KVH;
+  P.H = H;
+  P.KVH = KVH;
+  P.G = H / KVH;
+  P.n_tiles = (int)tiles_for(KVDEC_KIND_SPARSE, n);
+  P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
+  PagedSrc S{};
+  S.k = static_cast<const char*>(k_cache);
+  S.v = static_cast<const char*>(v_cache);
+  S.lens = seq_lens;
+  S.page_bytes = (int64_t)KVH * n * kRowBytes;
+  S.head_bytes = n * kRowBytes;
+  S.row_bytes = kRowBytes;
+  S.max_len = 0x3fffffff;
+  S.rows = (int)n;
+  S.window = window;
+  S.sink = sink;
+  S.layout = layout;
+  S.sparse = true;
   return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
 }
 

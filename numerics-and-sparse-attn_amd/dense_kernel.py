@@ -19,24 +19,51 @@ def dense_decode_attention(q, k, v, seq_len, sm_scale=None):
     """q: [BATCH, N_HEADS, D_HEAD]. k/v: [BATCH, N_KV_HEADS, seq_len, D_HEAD].
 
     Mirrors dense_kernel.py:70-82.  Shapes are read from the tensors and
-    checked (the reference takes them from constants.py); q, k, v are fp16
-    and contiguous; D_HEAD must be 128 and N_HEADS / N_KV_HEADS <= 16.
-    Asynchronous on torch's current stream.
+    checked (the reference takes them from constants.py); q, k, v are fp16,
+    D_HEAD must be 128 and N_HEADS / N_KV_HEADS <= 16.  Asynchronous on
+    torch's current stream.
+
+    Beyond the reference: ``seq_len`` may be a [BATCH] int32 tensor on the
+    GPU (per-sequence lengths; k / v are then [BATCH, N_KV_HEADS, L_max,
+    D_HEAD] and sequence b attends over its first seq_len[b] rows, a length
+    of 0 giving zeros), and k / v may be strided views (any strides with a
+    contiguous head dim, e.g. a permuted [BATCH, L, N_KV_HEADS, D_HEAD]
+    cache).  Both go through the strided kernel source; the contiguous,
+    scalar-length call is the reference's.
     """
     _checks.require_gpu_tensor("q", q, ndim=3)
-    _checks.require_gpu_tensor("k", k, ndim=4)
-    _checks.require_gpu_tensor("v", v, ndim=4)
+    _checks.require_gpu_tensor("k", k, ndim=4, contiguous=False)
+    _checks.require_gpu_tensor("v", v, ndim=4, contiguous=False)
     _checks.require_same_device(("q", q), ("k", k), ("v", v))
     B, H, D = q.shape
     KVH = k.shape[1]
-    seq_len = int(seq_len)
-    _checks.require_shape("k", k, (B, KVH, seq_len, D))
-    _checks.require_shape("v", v, (B, KVH, seq_len, D))
+    varlen = isinstance(seq_len, torch.Tensor)
+    if varlen:
+        _checks.seq_lens_tensor("seq_len", seq_len, B, q.device)
+        L = k.shape[2]
+    else:
+        L = seq_len = int(seq_len)
+    _checks.require_shape("k", k, (B, KVH, L, D))
+    _checks.require_shape("v", v, (B, KVH, L, D))
+    if not q.is_contiguous():
+        raise ValueError("q must be contiguous")
     o = torch.empty_like(q)
     if sm_scale is None:
         sm_scale = D_HEAD**-0.5
-    ws, nbytes = K.workspace(K.KIND_DENSE, B, H, KVH, seq_len, D, q.device)
-    rc = K.lib.kvdec_dense_decode(K.ptr(q), K.ptr(k), K.ptr(v), K.ptr(o), K.F16, B, H, KVH, seq_len,
-                                  D, float(sm_scale), K.ptr(ws), nbytes, K.stream_of(q))
+    ws, nbytes = K.workspace(K.KIND_DENSE, B, H, KVH, L, D, q.device)
+    if not varlen and k.is_contiguous() and v.is_contiguous():
+        rc = K.lib.kvdec_dense_decode(K.ptr(q), K.ptr(k), K.ptr(v), K.ptr(o), K.F16, B, H, KVH, L, D,
+                                      float(sm_scale), K.ptr(ws), nbytes, K.stream_of(q))
+        K.check(rc, "dense_decode_attention")
+        return o
+    _checks.row_major_rows("k", k)
+    _checks.row_major_rows("v", v)
+    if k.stride() != v.stride():
+        raise ValueError(f"k and v must share strides, got {k.stride()} and {v.stride()}")
+    sb, sh, sl, _ = k.stride()
+    rc = K.lib.kvdec_paged_decode(K.ptr(q), K.ptr(k), K.ptr(v), None,
+                                  K.ptr(seq_len) if varlen else None, K.ptr(o), K.F16, B, H, KVH, D,
+                                  L, 0, 0, 0, sb, sl, sh, float(sm_scale), K.ptr(ws), nbytes,
+                                  K.stream_of(q))
     K.check(rc, "dense_decode_attention")
     return o

@@ -23,7 +23,9 @@ def sparse_decode_attention(q, k_cache, v_cache, seq_len, window, sink=SINK_SIZE
     """k_cache/v_cache must be [BATCH, N_KV_HEADS, SINK+WINDOW, D_HEAD].
 
     Mirrors sparse_kernel.py:105-118 (same arguments and defaults; ``layout``
-    is an added keyword).  fp16, contiguous, D_HEAD == 128.
+    is an added keyword).  fp16, contiguous, D_HEAD == 128.  ``seq_len`` may
+    also be a [BATCH] int32 tensor on the GPU: each sequence is masked at
+    its own length (each >= 1).
     """
     _checks.require_gpu_tensor("q", q, ndim=3)
     _checks.require_gpu_tensor("k_cache", k_cache, ndim=4)
@@ -33,7 +35,12 @@ def sparse_decode_attention(q, k_cache, v_cache, seq_len, window, sink=SINK_SIZE
         raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {layout!r}")
     B, H, D = q.shape
     KVH = k_cache.shape[1]
-    window, sink, seq_len = int(window), int(sink), int(seq_len)
+    varlen = isinstance(seq_len, torch.Tensor)
+    if varlen:
+        _checks.seq_lens_tensor("seq_len", seq_len, B, q.device)
+    else:
+        seq_len = int(seq_len)
+    window, sink = int(window), int(sink)
     if window < 0 or sink < 0:
         raise ValueError(f"window and sink must be >= 0 (window={window}, sink={sink})")
     _checks.require_shape("k_cache", k_cache, (B, KVH, sink + window, D))
@@ -42,6 +49,13 @@ def sparse_decode_attention(q, k_cache, v_cache, seq_len, window, sink=SINK_SIZE
     if sm_scale is None:
         sm_scale = D_HEAD**-0.5
     ws, nbytes = K.workspace(K.KIND_SPARSE, B, H, KVH, sink + window, D, q.device)
+    if varlen:
+        rc = K.lib.kvdec_sparse_decode_varlen(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), K.ptr(o),
+                                              K.ptr(seq_len), K.F16, B, H, KVH, window, sink,
+                                              _LAYOUTS[layout], float(sm_scale), K.ptr(ws), nbytes,
+                                              K.stream_of(q))
+        K.check(rc, "sparse_decode_attention")
+        return o
     rc = K.lib.kvdec_sparse_decode(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), K.ptr(o), K.F16, B, H,
                                    KVH, seq_len, window, sink, _LAYOUTS[layout], float(sm_scale),
                                    K.ptr(ws), nbytes, K.stream_of(q))

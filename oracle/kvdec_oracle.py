@@ -195,6 +195,61 @@ def sparse_attention_compacted(q, k_cache, v_cache, seq_len, window, sink, sm_sc
 
 
 # --------------------------------------------------------------------------
+# Per-sequence lengths and paged caches (no counterpart in the reference,
+# which passes one scalar seq_len and a contiguous cache, dense_kernel.py:70-
+# 82 and sparse_kernel.py:105-118; each sequence reduces to those calls)
+# --------------------------------------------------------------------------
+
+def dense_attention_varlen(q, k, v, seq_lens, sm_scale, dtype=np.float64):
+    """Sequence b attends over rows [0, seq_lens[b]) of k[b], v[b]
+    ([B, KVH, L_max, D]); a length of 0 gives zeros."""
+    q = np.asarray(q)
+    out = np.zeros(q.shape, dtype=dtype)
+    for b, n in enumerate(np.asarray(seq_lens).tolist()):
+        if n > 0:
+            out[b] = dense_attention(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n], sm_scale, dtype)[0]
+    return out
+
+
+def sparse_attention_varlen(q, k_cache, v_cache, seq_lens, window, sink, sm_scale, layout=0,
+                            dtype=np.float64):
+    """sparse_attention_compacted per sequence, at that sequence's length."""
+    q = np.asarray(q)
+    out = np.zeros(q.shape, dtype=dtype)
+    for b, n in enumerate(np.asarray(seq_lens).tolist()):
+        out[b] = sparse_attention_compacted(q[b:b + 1], k_cache[b:b + 1], v_cache[b:b + 1], n, window,
+                                            sink, sm_scale, layout, dtype)[0]
+    return out
+
+
+def gather_pages(pages, block_row, n, layout="NHD"):
+    """Rows [0, n) of one sequence as [KVH, n, D]: token t is row t % P of
+    page block_row[t // P] (pages [num_pages, P, KVH, D] for "NHD",
+    [num_pages, KVH, P, D] for "HND")."""
+    pages = np.asarray(pages)
+    P = pages.shape[1] if layout == "NHD" else pages.shape[2]
+    t = np.arange(n)
+    page = np.asarray(block_row)[t // P]
+    if layout == "NHD":
+        rows = pages[page, t % P]                 # [n, KVH, D]
+        return np.swapaxes(rows, 0, 1)
+    return np.swapaxes(pages[page, :, t % P], 0, 1)   # [n, KVH, D] -> [KVH, n, D]
+
+
+def paged_attention(q, k_pages, v_pages, block_table, seq_lens, sm_scale, layout="NHD",
+                    dtype=np.float64):
+    """Dense decode of each sequence over its pages."""
+    q = np.asarray(q)
+    out = np.zeros(q.shape, dtype=dtype)
+    for b, n in enumerate(np.asarray(seq_lens).tolist()):
+        if n > 0:
+            kb = gather_pages(k_pages, block_table[b], n, layout)[None]
+            vb = gather_pages(v_pages, block_table[b], n, layout)[None]
+            out[b] = dense_attention(q[b:b + 1], kb, vb, sm_scale, dtype)[0]
+    return out
+
+
+# --------------------------------------------------------------------------
 # KIVI 2-bit quantizers
 # --------------------------------------------------------------------------
 

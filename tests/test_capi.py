@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 14
+    assert len(funcs) == 16
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -225,6 +225,55 @@ def test_stream_decode_validation():
     assert _sdecode(count=0) == E["WINDOW"]
     assert _sdecode(count=161) == E["WINDOW"]
     assert _sdecode(KVH=3) == E["SHAPE"]
+
+
+def _paged(**kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, bt=FAKE, lens=FAKE, o=FAKE, dtype=K.F16, B=4, H=64, KVH=8, D=128,
+             L=4096, ps=16, mb=256, np_=1024, sp=16 * 8 * 128, sr=8 * 128, sh=128, scale=0.088, ws=None,
+             nbytes=0, stream=None)
+    a.update(kw)
+    return K.lib.kvdec_paged_decode(a["q"], a["k"], a["v"], a["bt"], a["lens"], a["o"], a["dtype"],
+                                    a["B"], a["H"], a["KVH"], a["D"], a["L"], a["ps"], a["mb"],
+                                    a["np_"], a["sp"], a["sr"], a["sh"], a["scale"], a["ws"],
+                                    a["nbytes"], a["stream"])
+
+
+def test_paged_validation():
+    assert _paged(q=None) == E["NULL"]
+    assert _paged(v=None) == E["NULL"]
+    assert _paged(dtype=K.BF16) == E["DTYPE"]
+    assert _paged(D=64) == E["SHAPE"]
+    assert _paged(H=60) == E["SHAPE"]
+    assert _paged(L=0) == E["SEQLEN"]
+    assert _paged(L=1 << 30) == E["SHAPE"]
+    assert _paged(sr=-1) == E["SHAPE"]
+    assert _paged(sr=1 << 26) == E["SHAPE"]       # 16 rows past 2^31 bytes
+    assert _paged(ps=8) == E["UNSUPPORTED"]
+    assert _paged(ps=48) == E["UNSUPPORTED"]
+    assert _paged(mb=255) == E["SHAPE"]           # 255 * 16 < 4096 tokens
+    assert _paged(np_=0) == E["SHAPE"]
+    # B=4, L=4096 splits: a missing workspace is reported, nothing launched
+    assert _paged() == E["WORKSPACE"]
+    assert _paged(bt=None, ps=0, mb=0, np_=0) == E["WORKSPACE"]
+
+
+def _svarlen(**kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, lens=FAKE, dtype=K.F16, B=4, H=64, KVH=8, W=16384, S=4,
+             layout=K.LAYOUT_LINEAR, scale=0.088, ws=None, nbytes=0, stream=None)
+    a.update(kw)
+    return K.lib.kvdec_sparse_decode_varlen(a["q"], a["k"], a["v"], a["o"], a["lens"], a["dtype"],
+                                            a["B"], a["H"], a["KVH"], a["W"], a["S"], a["layout"],
+                                            a["scale"], a["ws"], a["nbytes"], a["stream"])
+
+
+def test_sparse_varlen_validation():
+    assert _svarlen(lens=None) == E["NULL"]
+    assert _svarlen(dtype=K.F32) == E["DTYPE"]
+    assert _svarlen(W=0, S=0) == E["WINDOW"]
+    assert _svarlen(W=-1) == E["WINDOW"]
+    assert _svarlen(layout=5) == E["UNSUPPORTED"]
+    assert _svarlen(layout=K.LAYOUT_RING, W=0) == E["WINDOW"]
+    assert _svarlen() == E["WORKSPACE"]
 
 
 def _build(**kw):

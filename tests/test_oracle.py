@@ -110,6 +110,87 @@ def test_masked_attention_ignores_invalid_contents():
 
 
 # ----------------------------------------------------------------------------
+# per-sequence lengths and paged caches
+# ----------------------------------------------------------------------------
+
+def test_dense_varlen_brute_force_and_garbage():
+    """Each sequence equals brute force over its own first rows; rows past
+    the length (NaN here) and a length of 0 (zeros) never leak in."""
+    r = _rng(11)
+    q = r.standard_normal((3, 4, 5))
+    k = r.standard_normal((3, 2, 9, 5))
+    v = r.standard_normal((3, 2, 9, 5))
+    lens = [9, 4, 0]
+    got = O.dense_attention_varlen(q, k, v, lens, 0.4)
+    for b, n in enumerate(lens[:2]):
+        want = _brute_dense(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n], 0.4)
+        np.testing.assert_allclose(got[b:b + 1], want, rtol=1e-12, atol=1e-12)
+    assert np.all(got[2] == 0)
+    k2, v2 = k.copy(), v.copy()
+    k2[1, :, 4:] = np.nan
+    v2[1, :, 4:] = np.nan
+    np.testing.assert_array_equal(O.dense_attention_varlen(q, k2, v2, lens, 0.4), got)
+
+
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+def test_paged_gather_known_answer(layout):
+    """Token t of a sequence is row t % P of page table[t // P]: hand-placed
+    rows come back in order, and a wrong index (page-major vs row-major,
+    heads and tokens swapped) would not."""
+    P, KVH, D, num_pages = 4, 2, 3, 5
+    shape = (num_pages, P, KVH, D) if layout == "NHD" else (num_pages, KVH, P, D)
+    pages = np.zeros(shape)
+    table = [3, 0, 4]
+    for t in range(10):
+        for h in range(KVH):
+            val = [1000 * h + t, -t, h]
+            if layout == "NHD":
+                pages[table[t // P], t % P, h] = val
+            else:
+                pages[table[t // P], h, t % P] = val
+    got = O.gather_pages(pages, table, 10, layout)
+    assert got.shape == (KVH, 10, D)
+    for t in range(10):
+        for h in range(KVH):
+            assert list(got[h, t]) == [1000 * h + t, -t, h]
+
+
+def test_paged_attention_equals_varlen_after_scatter():
+    r = _rng(12)
+    B, H, KVH, D, L, P = 3, 4, 2, 8, 21, 4
+    q = r.standard_normal((B, H, D))
+    k = r.standard_normal((B, KVH, L, D))
+    v = r.standard_normal((B, KVH, L, D))
+    lens = [21, 5, 0]
+    nb = (L + P - 1) // P
+    perm = r.permutation(B * nb)
+    table = perm.reshape(B, nb)
+    kp = r.standard_normal((B * nb, P, KVH, D)) * 1e3
+    vp = r.standard_normal((B * nb, P, KVH, D)) * 1e3
+    for b in range(B):
+        for t in range(lens[b]):
+            kp[table[b, t // P], t % P] = k[b, :, t]
+            vp[table[b, t // P], t % P] = v[b, :, t]
+    np.testing.assert_allclose(O.paged_attention(q, kp, vp, table, lens, 0.3),
+                               O.dense_attention_varlen(q, k, v, lens, 0.3), rtol=1e-12, atol=1e-12)
+
+
+def test_sparse_varlen_is_per_sequence_call():
+    r = _rng(13)
+    B, H, KVH, D, W, S = 3, 4, 2, 8, 6, 2
+    q = r.standard_normal((B, H, D))
+    kc = r.standard_normal((B, KVH, S + W, D))
+    vc = r.standard_normal((B, KVH, S + W, D))
+    lens = [1, 5, 40]
+    got = O.sparse_attention_varlen(q, kc, vc, lens, W, S, 0.5)
+    for b, n in enumerate(lens):
+        want = O.sparse_attention_compacted(q[b:b + 1], kc[b:b + 1], vc[b:b + 1], n, W, S, 0.5)
+        np.testing.assert_array_equal(got[b:b + 1], want)
+    # length 1: only sink slot 0 is valid, so the output is V[slot 0]
+    np.testing.assert_allclose(got[0], np.repeat(vc[0, :, 0], H // KVH, axis=0), rtol=1e-12)
+
+
+# ----------------------------------------------------------------------------
 # StreamingLLM sink + window
 # ----------------------------------------------------------------------------
 
