@@ -1,7 +1,7 @@
 """Decode-attention benchmark on one MI355X: prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--paths kivi,dense,sparse,quantize,sweep,stream]
+                    [--paths kivi,dense,sparse,quantize,sweep,stream,paged]
                     [--no-cpu] [--no-latency]
 
 Workload (the BASELINE metric's configuration): B=32, 64 query / 8 KV heads,
@@ -19,6 +19,9 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
             reserve the next token's ring row (quantizing a block every 32
             steps), then attend; each cache advances 32 steps, so the time
             includes one eviction per 32 steps
+  paged     the dense L=163840 cache scattered over 16-token pages in a
+            random order (vLLM's [pages, 16, KVH, D] layout), decoded through
+            block tables and per-sequence lengths (paged_kernel.py)
 
 Timing.  Each path keeps several independent input sets resident in HBM
 (together >= 1 GiB, more than L2 plus the 256 MB Infinity Cache) and captures
@@ -106,6 +109,11 @@ def bytes_stream_step(window, residual=R):
     attend = bytes_kivi(window, residual) + pairs * 2 * 15.5 * D * 2
     evict = pairs * (2 * 32 * D * 2 + 2 * (32 * D // 4) + 2 * 2 * D + 2 * 2 * 32 * (D // 32))
     return int(append + attend + evict / 32)
+
+
+def bytes_paged(n_tok, page_size):
+    """bytes_dense plus the block table and the per-sequence lengths."""
+    return bytes_dense(n_tok) + B * (-(-n_tok // page_size)) * 4 + B * 4
 
 
 def bytes_quantize(n_tok):
@@ -251,7 +259,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--paths", default="kivi,dense,sparse,quantize,sweep,stream")
+    ap.add_argument("--paths", default="kivi,dense,sparse,quantize,sweep,stream,paged")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-latency", action="store_true", help="skip the per-call latency runs")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -365,11 +373,12 @@ def main():
         out["sparse_fp16_w256"] = path_record(ms, bytes_sparse(W), ns, K, latency=lat)
         del sets
 
-    if "quantize" in paths or "dense" in paths:
+    if "quantize" in paths or "dense" in paths or "paged" in paths:
         k = randn(B, KVH, L, D)
         k[..., outliers] *= 10
         v = randn(B, KVH, L, D)
         q = randn(B, H, D)
+        dsteps = max(3, K // 5)
         if "quantize" in paths:
             qsteps = max(3, K // 10)
             ms, _ = graph_time(lambda i: quant_kernel.quantize_k_cache(k), 1, qsteps, 1)
@@ -377,7 +386,6 @@ def main():
             ms, _ = graph_time(lambda i: quant_kernel.quantize_v_cache(v), 1, qsteps, 1)
             out["quantize_v_L163840"] = path_record(ms, bytes_quantize(L), 1, qsteps)
         if "dense" in paths:
-            dsteps = max(3, K // 5)
             ms, _ = graph_time(lambda i: dense_kernel.dense_decode_attention(q, k, v, seq_len=L), 1,
                                dsteps, 1)
             out["dense_L163840"] = path_record(ms, bytes_dense(L), 1, dsteps)
@@ -387,9 +395,29 @@ def main():
                     "value": round(us, 1), "unit": "us/step", "cores": _blas_threads(), "kind": "port",
                     "sample": f"batch row 0 of 32 at L=163840 (numpy oracle, float32, median of "
                               f"{reps} reps), scaled x32"}
+        if "paged" in paths:
+            # the same cache scattered over 16-token pages ([pages, 16, KVH,
+            # D], vLLM's layout) in a random order, every sequence at full
+            # length through per-sequence lengths
+            import paged_kernel
+            ps = 16
+            nb = L // ps
+            table = torch.randperm(B * nb, generator=torch.Generator().manual_seed(1)).to(dev)
+            table = table.view(B, nb).to(torch.int32)
+            idx = table.view(-1).long()
+            kp = torch.empty(B * nb, ps, KVH, D, dtype=torch.float16, device=dev)
+            kp[idx] = k.view(B, KVH, nb, ps, D).permute(0, 2, 3, 1, 4).reshape(-1, ps, KVH, D)
+            vp = torch.empty_like(kp)
+            vp[idx] = v.view(B, KVH, nb, ps, D).permute(0, 2, 3, 1, 4).reshape(-1, ps, KVH, D)
+            lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+            ms, _ = graph_time(lambda i: paged_kernel.paged_decode_attention(
+                q, kp, vp, table, lens, max_seq_len=L, kv_layout="NHD"), 1, dsteps, 1)
+            out["paged_nhd16_L163840"] = path_record(ms, bytes_paged(L, ps), 1, dsteps)
+            del kp, vp, table, idx, lens
+        del k, v
+        if "dense" in paths:
             # config 2: L = 32768 (a prefix view of the same cache would not be
             # contiguous, so the cache is regenerated at that length)
-            del k, v
             Ls = 32768
             ns = n_sets(bytes_dense(Ls))
             dsets = [(randn(B, H, D), randn(B, KVH, Ls, D), randn(B, KVH, Ls, D)) for _ in range(ns)]
@@ -401,8 +429,6 @@ def main():
             ms, _ = graph_time(dcall, ns, max(3, K // 2), 1)
             out["dense_L32768"] = path_record(ms, bytes_dense(Ls), ns, max(3, K // 2))
             del dsets
-        else:
-            del k, v
 
     head_key = "kivi_w256" if "kivi_w256" in out else next(iter(out))
     head = out[head_key]

@@ -79,20 +79,25 @@ struct F16Items {
   typedef F16Raw Raw;
   rsrc_t rk, rv;
   int tile0, n, slot_base;
+  int rot;        // queue item i is tile (i + rot) mod n
   SlotRanges R;   // loads of tiles with no valid slot are skipped
+  __device__ __forceinline__ int tile(int i) const {
+    const int j = i + rot;
+    return tile0 + (j >= n ? j - n : j);
+  }
   __device__ __forceinline__ void load(int i, Raw& X, int lane) const {
-    const bool live = i < n && tile_any_valid(R, slot_base + kTile * (tile0 + i));
-    load_f16(rk, rv, live ? (uint32_t)(tile0 + i) * kSlotBytes : kOOB, lane, X);
+    const bool live = i < n && tile_any_valid(R, slot_base + kTile * tile(i));
+    load_f16(rk, rv, live ? (uint32_t)tile(i) * kSlotBytes : kOOB, lane, X);
   }
   typedef WaveState State;
   __device__ __forceinline__ void step(int i, const Raw& X, State& st, const StepCtx& c) const {
-    f16_tile_step(X, c.slot, c.qB, slot_base + kTile * (tile0 + i), c.R, c.scale_log2, st, c.lane);
+    f16_tile_step(X, c.slot, c.qB, slot_base + kTile * tile(i), c.R, c.scale_log2, st, c.lane);
   }
   // The same, in a wave whose quantized-tile accumulators qs share st.m.
   __device__ __forceinline__ void step(int i, const Raw& X, State& st, QState& qs,
                                        const StepCtx& c) const {
     const int lane = c.lane;
-    f16_tile_step(X, c.slot, c.qB, slot_base + kTile * (tile0 + i), c.R, c.scale_log2, st, lane,
+    f16_tile_step(X, c.slot, c.qB, slot_base + kTile * tile(i), c.R, c.scale_log2, st, lane,
                   [&](float alpha) { q_state_rescale(qs, alpha, lane); });
   }
 };
@@ -338,6 +343,12 @@ struct F16Src {
     it.tile0 = split * P.tiles_per_split;
     it.n = min(P.tiles_per_split, P.n_tiles - it.tile0);
     it.slot_base = 0;
+    it.rot = 0;
+    // Unit u starts its stream u tiles into its region (wrapping), so that
+    // the 256 concurrent streams, whose regions start at multiples of the
+    // same large stride, do not sweep the same address offsets in lockstep
+    // (1.8% at L = 163840).
+    if (it.n > 0) it.rot = (int)((uint64_t)pair % (uint64_t)it.n);
     it.R = P.R;
     Ring<F16Items> ring;
     ring_begin(it, ring, wave, wave + kWaves, lane);
@@ -556,6 +567,7 @@ struct KiviSrc {
       rit.tile0 = 0;
       rit.n = n_res();
       rit.slot_base = sink + win_tok;
+      rit.rot = 0;
       rit.R = P.R;
       bool has_q = false;
       if (nqw > 0) {
