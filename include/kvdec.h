@@ -191,6 +191,20 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
                              void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * kvdec_sparse_decode_kivi with one length per sequence (seq_lens [B] int32
+ * on the device, each >= 1; the reference passes one scalar,
+ * quant_kernel.py:551-581): each sequence's slots are masked by the
+ * _kv_indices rule at its own length, so sequences in ramp-up and in steady
+ * state share one launch.  Same cache tensors and limits; no workspace.
+ */
+int kvdec_sparse_decode_kivi_varlen(const void* q, const void* k_res, const void* v_res,
+                                    const void* const* kivi, void* o,
+                                    const int32_t* seq_lens, int64_t B, int32_t H,
+                                    int32_t KVH, int32_t window, int32_t sink,
+                                    int32_t residual, int32_t group, int32_t bits,
+                                    float sm_scale, void* stream);
+
+/*
  * Decode-time KIVI cache, the write side of the fused decode (no counterpart
  * in the reference, which builds the cache once per call:
  * quant_kernel.py:584-622).  State per (b, kv) head: the quantized sink

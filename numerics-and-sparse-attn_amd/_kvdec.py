@@ -53,6 +53,9 @@ SIGNATURES = {
     "kvdec_sparse_decode_kivi": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _i64, _i32,
                                                 _i32, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _vp,
                                                 _sz, _vp]),
+    "kvdec_sparse_decode_kivi_varlen": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _vp, _i64,
+                                                       _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                                                       _vp]),
     "kvdec_kivi_stream_append": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.POINTER(_vp), _i64, _i32,
                                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "kvdec_kivi_stream_decode": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _i64, _i32,

@@ -484,8 +484,11 @@ struct PagedSrc {
 };
 
 // KIVI cache: the fp16 residual (slots sink + win_tok ..) and the quantized
-// sink and window-old groups.
-struct KiviSrc {
+// sink and window-old groups.  VARLEN: each sequence's slot validity comes
+// from its own length lens[b] instead of P.R (a separate instantiation, so
+// the one-length kernel carries none of it).
+template <bool VARLEN>
+struct KiviSrcBase {
   const _Float16* kres;
   const _Float16* vres;
   int res_rows;
@@ -494,6 +497,8 @@ struct KiviSrc {
   int sink;
   int win_tok;     // window - residual
   int nwt;         // win_tok / 32
+  const int32_t* lens;   // VARLEN: per-sequence lengths [B]
+  int window;
 
   // Work split.  While the residual has at most kWaves tiles, the first nrw
   // waves take one residual tile each and the other nqw waves are quantized
@@ -521,6 +526,9 @@ struct KiviSrc {
   __device__ __forceinline__ void process(int64_t pair, int, const AttnCommon& P, int wave,
                                           int lane, int* ctr, Sync&& sync, WaveState& st) const {
     const int nrw = n_res_waves();
+    SlotRanges R = P.R;
+    if constexpr (VARLEN)
+      R = sparse_ranges(max((int)((cint32*)lens)[pair / P.KVH], 0), window, sink, KVDEC_LAYOUT_LINEAR);
     QRegion S = sinkq, Wq = winq;
     S.kp += (size_t)pair * 8 * kHeadDim;
     S.ks += (size_t)pair * kHeadDim;
@@ -568,7 +576,7 @@ struct KiviSrc {
       rit.n = n_res();
       rit.slot_base = sink + win_tok;
       rit.rot = 0;
-      rit.R = P.R;
+      rit.R = R;
       bool has_q = false;
       if (nqw > 0) {
         // one extra quantized tile (if there is one) and one residual tile.
@@ -581,17 +589,19 @@ struct KiviSrc {
         const int qe = nqw + rw;
         qonly.load(qe, E, lane);
         sync(c, true);
-        F16Raw R;
-        rit.load(rw, R, lane);
+        if constexpr (VARLEN) c.R = R;
+        F16Raw X;
+        rit.load(rw, X, lane);
         if (qe < qonly.n) {
           qonly.step(qe, E, qref, c);
           has_q = true;
         }
-        rit.step(rw, R, st, qs, c);
+        rit.step(rw, X, st, qs, c);
       } else {
         Ring<F16Items> rring;
         ring_begin(rit, rring, rw, rw + nrw, lane);
         sync(c, dyn);
+        if constexpr (VARLEN) c.R = R;
         if (rit.n > 2 * nrw)
           ring_run_dynamic(rit, rring, ctr, st, c);
         else
@@ -614,6 +624,7 @@ struct KiviSrc {
       Ring<QItems<false>> qring;
       ring_begin(qonly, qring, qw, qw + nqw + nrw, lane);
       sync(c, dyn || nqw > 0);
+      if constexpr (VARLEN) c.R = R;
       if (dyn_q)
         ring_run_dynamic(qonly, qring, ctr + 1, qref, c);
       else
@@ -623,6 +634,9 @@ struct KiviSrc {
     }
   }
 };
+
+struct KiviSrc : KiviSrcBase<false> {};
+struct KiviVarSrc : KiviSrcBase<true> {};
 
 template <class Src>
 __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) {
@@ -770,6 +784,76 @@ int launch_attn(AttnCommon P, const Src& S, bool kivi, size_t ws_bytes, hipStrea
   const int64_t outs = P.pairs * P.G * kHeadDim;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, stream, P);
   return launch_status();
+}
+
+// The fused KIVI decode at one length (lens null) or at per-sequence
+// lengths lens[b] (seq_len unused).
+int kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
+                void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH, int64_t seq_len,
+                int32_t window, int32_t sink, int32_t residual, int32_t group, int32_t bits,
+                float sm_scale, void* stream) {
+  if (!q || !k_res || !v_res || !kivi || !o) return KVDEC_E_NULL;
+  if (bits != 2) return KVDEC_E_BITS;
+  if (group != 32) return KVDEC_E_UNSUPPORTED;
+  int rc = check_heads(B, H, KVH, kHeadDim);
+  if (rc) return rc;
+  if (seq_len < 1) return KVDEC_E_SEQLEN;
+  if (sink < 1 || sink > group || residual < kTile || residual % kTile != 0 || window < 1)
+    return KVDEC_E_WINDOW;
+  // A window shorter than the residual stays fp16 entirely (residual rows =
+  // window, no window-old tokens).
+  const int32_t res_rows = window < residual ? window : residual;
+  const int32_t win_tok = window - res_rows;
+  if (win_tok % group != 0) return KVDEC_E_GROUP;
+  for (int i = 0; i < 6; ++i)
+    if (!kivi[i]) return KVDEC_E_NULL;
+  if (win_tok > 0)
+    for (int i = 6; i < 12; ++i)
+      if (!kivi[i]) return KVDEC_E_NULL;
+  if ((int64_t)res_rows * kRowBytes >= ((int64_t)1 << 31) ||
+      (int64_t)win_tok * kHeadDim >= ((int64_t)1 << 31))
+    return KVDEC_E_SHAPE;
+
+  AttnCommon P{};
+  P.q = static_cast<const _Float16*>(q);
+  P.o = static_cast<_Float16*>(o);
+  P.ws = nullptr;
+  P.pairs = B * KVH;
+  P.H = H;
+  P.KVH = KVH;
+  P.G = H / KVH;
+  P.n_tiles = (int)tiles_for(KVDEC_KIND_KIVI, window);
+  P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
+  P.R = sparse_ranges(seq_len, window, sink, KVDEC_LAYOUT_LINEAR);
+
+  auto u8 = [&](int i) { return static_cast<const uint8_t*>(kivi[i]); };
+  auto f16 = [&](int i) { return static_cast<const _Float16*>(kivi[i]); };
+  KiviVarSrc S{};
+  S.kres = static_cast<const _Float16*>(k_res);
+  S.vres = static_cast<const _Float16*>(v_res);
+  S.res_rows = res_rows;
+  S.sinkq = QRegion{u8(0), f16(1), f16(2), u8(3), f16(4), f16(5)};
+  if (win_tok > 0)
+    S.winq = QRegion{u8(6), f16(7), f16(8), u8(9), f16(10), f16(11)};
+  else
+    S.winq = S.sinkq;   // never dereferenced: there are no window-old tiles
+  S.sink = sink;
+  S.win_tok = win_tok;
+  S.nwt = win_tok / kTile;
+  S.lens = lens;
+  S.window = window;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (lens) return launch_attn(P, S, true, 0, st);
+  KiviSrc S1{};
+  S1.kres = S.kres;
+  S1.vres = S.vres;
+  S1.res_rows = S.res_rows;
+  S1.sinkq = S.sinkq;
+  S1.winq = S.winq;
+  S1.sink = S.sink;
+  S1.win_tok = S.win_tok;
+  S1.nwt = S.nwt;
+  return launch_attn(P, S1, true, 0, st);
 }
 
 }  // namespace
@@ -956,57 +1040,20 @@ int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res
                              int64_t seq_len, int32_t window, int32_t sink, int32_t residual,
                              int32_t group, int32_t bits, float sm_scale, void* ws,
                              size_t ws_bytes, void* stream) {
-  if (!q || !k_res || !v_res || !kivi || !o) return KVDEC_E_NULL;
-  if (bits != 2) return KVDEC_E_BITS;
-  if (group != 32) return KVDEC_E_UNSUPPORTED;
-  int rc = check_heads(B, H, KVH, kHeadDim);
-  if (rc) return rc;
-  if (seq_len < 1) return KVDEC_E_SEQLEN;
-  if (sink < 1 || sink > group || residual < kTile || residual % kTile != 0 || window < 1)
-    return KVDEC_E_WINDOW;
-  // A window shorter than the residual stays fp16 entirely (residual rows =
-  // window, no window-old tokens).
-  const int32_t res_rows = window < residual ? window : residual;
-  const int32_t win_tok = window - res_rows;
-  if (win_tok % group != 0) return KVDEC_E_GROUP;
-  for (int i = 0; i < 6; ++i)
-    if (!kivi[i]) return KVDEC_E_NULL;
-  if (win_tok > 0)
-    for (int i = 6; i < 12; ++i)
-      if (!kivi[i]) return KVDEC_E_NULL;
-  if ((int64_t)res_rows * kRowBytes >= ((int64_t)1 << 31) ||
-      (int64_t)win_tok * kHeadDim >= ((int64_t)1 << 31))
-    return KVDEC_E_SHAPE;
-  (void)ws;
+  (void)ws;         // one pass: no workspace
   (void)ws_bytes;
+  return kivi_decode(q, k_res, v_res, kivi, o, nullptr, B, H, KVH, seq_len, window, sink, residual,
+                     group, bits, sm_scale, stream);
+}
 
-  AttnCommon P{};
-  P.q = static_cast<const _Float16*>(q);
-  P.o = static_cast<_Float16*>(o);
-  P.ws = nullptr;
-  P.pairs = B * KVH;
-  P.H = H;
-  P.KVH = KVH;
-  P.G = H / KVH;
-  P.n_tiles = (int)tiles_for(KVDEC_KIND_KIVI, window);
-  P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
-  P.R = sparse_ranges(seq_len, window, sink, KVDEC_LAYOUT_LINEAR);
-
-  auto u8 = [&](int i) { return static_cast<const uint8_t*>(kivi[i]); };
-  auto f16 = [&](int i) { return static_cast<const _Float16*>(kivi[i]); };
-  KiviSrc S{};
-  S.kres = static_cast<const _Float16*>(k_res);
-  S.vres = static_cast<const _Float16*>(v_res);
-  S.res_rows = res_rows;
-  S.sinkq = QRegion{u8(0), f16(1), f16(2), u8(3), f16(4), f16(5)};
-  if (win_tok > 0)
-    S.winq = QRegion{u8(6), f16(7), f16(8), u8(9), f16(10), f16(11)};
-  else
-    S.winq = S.sinkq;   // never dereferenced: there are no window-old tiles
-  S.sink = sink;
-  S.win_tok = win_tok;
-  S.nwt = win_tok / kTile;
-  return launch_attn(P, S, true, ws_bytes, static_cast<hipStream_t>(stream));
+int kvdec_sparse_decode_kivi_varlen(const void* q, const void* k_res, const void* v_res,
+                                    const void* const* kivi, void* o, const int32_t* seq_lens,
+                                    int64_t B, int32_t H, int32_t KVH, int32_t window,
+                                    int32_t sink, int32_t residual, int32_t group, int32_t bits,
+                                    float sm_scale, void* stream) {
+  if (!seq_lens) return KVDEC_E_NULL;
+  return kivi_decode(q, k_res, v_res, kivi, o, seq_lens, B, H, KVH, 1, window, sink, residual,
+                     group, bits, sm_scale, stream);
 }
 
 int kvdec_kivi_stream_decode(const void* q, const void* k_ring, const void* v_ring,

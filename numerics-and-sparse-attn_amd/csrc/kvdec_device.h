@@ -193,13 +193,18 @@ __device__ __forceinline__ void tile_body(KOp&& kop, VOp&& vop, uint32_t valid,
     st.m = mnew;
   }
 
-  half8 pB;
+  // p = pB + pL: the fp16 head and the fp16 rounding of the remainder (the
+  // remainder is exact in fp32), so the PV product carries p to ~2^-22
+  // instead of fp16's 2^-11 (one dominant token would otherwise put that
+  // whole rounding error into the output).
+  half8 pB, pL;
   float ls = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float p = __builtin_amdgcn_exp2f(x[j] - st.m);
     ls += p;
     pB[j] = (_Float16)p;
+    pL[j] = (_Float16)__builtin_fmaf(-1.0f, (float)pB[j], p);
   }
   st.l += ls;
 
@@ -217,6 +222,7 @@ __device__ __forceinline__ void tile_body(KOp&& kop, VOp&& vop, uint32_t valid,
       a[2] = __builtin_amdgcn_perm(d[5], d[4], sel);
       a[3] = __builtin_amdgcn_perm(d[7], d[6], sel);
       st.O[2 * w + e] = mfma16x16x32(a, pB, st.O[2 * w + e]);
+      st.O[2 * w + e] = mfma16x16x32(a, pL, st.O[2 * w + e]);
     }
   }
 }
@@ -320,12 +326,13 @@ __device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, bool valid,
 // share).  The PV product of a quantized tile is computed transposed,
 // O[head][channel] = P'[head][token] . (code - zero)[token][channel], with
 // each MFMA covering 16 channels of one 32-channel V quantization group, so
-// the per-token V scale folds into P' = p * scale.  The B operands are exact
-// fp16 subnormals: the code as it sits in its byte (code * 4^k, k = t % 4,
-// the channel's position in the byte) times 2^-24, and, in a second MFMA,
-// -zero * 4^k * 2^-24.
-//   O[blk][r] : 4^k 2^-24 sum_t P'[t][head 4g + r] * (code - zero)[t][channel
-//               16 blk + t] for lane (t, g); q_state_scale() is 2^24 / 4^k
+// the per-token V scale folds into P' = p * scale.  The B operand is the
+// code as it sits in its byte (code * 4^k, k = t % 4, the channel's position
+// in the byte) minus zero * 4^k, times 2^-8: exact normal fp16 values (the
+// MFMA rounds products of fp16 subnormals to about 2^-13, so the operand is
+// kept out of the subnormal range).
+//   O[blk][r] : 4^k 2^-8 sum_t P'[t][head 4g + r] * (code - zero)[t][channel
+//               16 blk + t] for lane (t, g); q_state_scale() is 2^8 / 4^k
 struct QState {
   float4v O[8];
 };
@@ -337,7 +344,7 @@ __device__ __forceinline__ void q_state_init(QState& qs) {
 
 // Factor that turns the lane's accumulators into output values.
 __device__ __forceinline__ float q_state_scale(int lane) {
-  return __builtin_ldexpf(1.0f, 24 - 2 * (lane & 3));
+  return __builtin_ldexpf(1.0f, 8 - 2 * (lane & 3));
 }
 
 // Rescale by alpha, given per head in lane layout (head = lane & 15); the
@@ -386,11 +393,9 @@ __device__ __forceinline__ uint32_t codes_1024(uint32_t c, uint32_t sel) {
 }
 
 // Consume one KIVI tile staged in the wave's LDS slot.
-//   QK: K is dequantized to fp16 as (code - zero) * scale.  fp16 patterns
-//       0x6400 | code are 1024 + code exactly; adding -(1024 + zero) gives
-//       code - zero exactly, and since min/max quantization keeps |code -
-//       zero| <= 2 except in rare groups, the product with the fp16 scale is
-//       the reference's value exactly.
+//   QK: fp16 patterns 0x6400 | code are 1024 + code exactly; adding
+//       -(1024 + zero) gives code - zero exactly (the A operand), and the
+//       per-channel K scale goes to the Q side (see below).
 //   softmax: the reference max is refreshed when the tile's max exceeds it
 //       by more than `slack`: kRescaleSlack when every V scale of the tile
 //       is at most kSlackVScale (then p <= 2^8 and P' = p * vscale < 2^15
@@ -400,9 +405,13 @@ __device__ __forceinline__ uint32_t codes_1024(uint32_t c, uint32_t sel) {
 // Without MIXED, st.O must be zero.  HALF: only tokens 0..15 can be valid (the sink
 // group), so the second 16-token block is skipped in QK and fed as zeros to
 // PV.  Masked tokens get p = 0; their codes are finite.
+//   FOLD: every V zero of the tile has |zero| <= kFoldZeroMax, so
+//       (code - zero) * 4^k * 2^-8 is one exact fp16 (one MFMA pair per
+//       16 channels); otherwise code and zero go through separate MFMAs.
 constexpr float kSlackVScale = 128.0f;
+constexpr float kFoldZeroMax = 1000.0f;
 
-template <bool MIXED, bool HALF>
+template <bool MIXED, bool HALF, bool FOLD>
 __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[4], int slot0,
                                             int xlim, const SlotRanges& R, float scale_log2,
                                             float slack, WaveState& st, QState& qs, int lane) {
@@ -417,11 +426,17 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   }
 
   // S[token][head] on MFMA: lane (t, g) feeds token 16 blk + t, channels
-  // 32c + 8g .. +7 (code byte row (16 blk + t) / 4, bits 2 (t % 4))
+  // 32c + 8g .. +7 (code byte row (16 blk + t) / 4, bits 2 (t % 4)) as the
+  // exact small integer code - zero; the per-channel K scale goes to the Q
+  // side as q * scale = head + remainder, both fp16 (the remainder of an
+  // fp16 x fp16 product is exact in fp16), so the logits carry the
+  // dequantized K exactly instead of fp16 roundings of scale * (code - zero).
   const uint32_t sh = 2u * (uint32_t)(t & 3);
   float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
+    const half8 qh = qB[c] * ks[c];
+    const half8 ql = __builtin_elementwise_fma(qB[c], ks[c], -qh);
 #pragma unroll
     for (int blk = 0; blk < (HALF ? 1 : 2); ++blk) {
       const u32x2 w =
@@ -432,11 +447,13 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
                        pk_sub_f16(codes_1024(c0, 0x00070006u), kz1[c][1]),
                        pk_sub_f16(codes_1024(c1, 0x00050004u), kz1[c][2]),
                        pk_sub_f16(codes_1024(c1, 0x00070006u), kz1[c][3])};
-      const u32x4 a = as_u4(as_h8(d) * ks[c]);
-      if (blk == 0)
-        s0 = mfma16x16x32(a, qB[c], s0);
-      else
-        s1 = mfma16x16x32(a, qB[c], s1);
+      if (blk == 0) {
+        s0 = mfma16x16x32(d, qh, s0);
+        s0 = mfma16x16x32(d, ql, s0);
+      } else {
+        s1 = mfma16x16x32(d, qh, s1);
+        s1 = mfma16x16x32(d, ql, s1);
+      }
     }
   }
 
@@ -461,53 +478,65 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
     q_state_rescale(qs, alpha, lane);
     st.m = mnew;
   }
+  float pf[8];
   half8 pB;
   float ls = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float p = __builtin_amdgcn_exp2f(x[j] - st.m);
-    ls += p;
-    pB[j] = (_Float16)p;
+    pf[j] = __builtin_amdgcn_exp2f(x[j] - st.m);
+    ls += pf[j];
+    pB[j] = (_Float16)pf[j];
   }
   st.l += ls;
 
-  // P' per V group, and -zero * 4^k * 2^-24 for the lane's tokens:
-  // tau(g, 0..3) = 4g..4g+3 and tau(g, 4..7) = 16 + 4g .. +3 sit
-  // contiguously in the transposed rows.  Both products are exact (the zero
-  // is an integer of at most 11 bits).
-  const _Float16 zk = (_Float16)(-__builtin_ldexpf(1.0f, 2 * (t & 3) - 24));
-  half8 pq[4];
-  u32x4 zz[4];
+  // P' = p * scale per V group as an fp16 head pq + fp16 remainder pl (as
+  // for fp16 tiles).  tau(g, 0..3) = 4g..4g+3 and tau(g, 4..7) =
+  // 16 + 4g .. +3 sit contiguously in the transposed rows.
+  const _Float16 k4 = (_Float16)__builtin_ldexpf(1.0f, 2 * (t & 3) - 8);   // 4^k 2^-8
+  const uint32_t vmask = 0x03030303u << sh;
+  // PV, one V group (two 16-channel blocks) at a time: lane (t, g) feeds
+  // channel 16 blk + t of the tokens tau(g, j) (transposed code byte row
+  // 4 blk + t/4, bits 2k, 2k + 1 with k = t % 4).  The masked byte in the
+  // low byte of 0x64xx is the fp16 1024 + code * 4^k; times 2^-8 that is
+  // 4 + code * 4^k * 2^-8, so one fused multiply-add against
+  // 4 + zero * 4^k * 2^-8 (FOLD) or 4 leaves the exact operand.  Each
+  // product is taken with the head and the remainder of P'.
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
     const u32x2 s_lo = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 8 * g);
     const u32x2 s_hi = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 32 + 8 * g);
     const u32x2 z_lo = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 8 * g);
     const u32x2 z_hi = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 32 + 8 * g);
-    pq[grp] = pB * as_h8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
-    zz[grp] = as_u4(as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]}) * zk);
-  }
-
-  // PV: lane (t, g) feeds channel 16 blk + t of the tokens tau(g, j)
-  // (transposed code byte row 4 blk + t/4, bits 2k, 2k + 1 with k = t % 4).
-  // The masked byte goes into the low byte of an fp16 whose high byte is
-  // zero: the subnormal code * 4^k * 2^-24.  The second MFMA adds the zero
-  // term with the same factor.
-  const uint32_t vmask = 0x03030303u << sh;
+    const half8 vsc = as_h8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
+    // head: fp16 product of the fp16 p and scale; remainder: the exact
+    // p * scale - head, rounded once (one fused multiply-add)
+    const half8 pq = pB * vsc;
+    half8 pl;
 #pragma unroll
-  for (int blk = 0; blk < 8; ++blk) {
-    const char* row = slot + kQsV + (4 * blk + (t >> 2)) * 32;
-    const uint32_t c0 = *reinterpret_cast<const uint32_t*>(row + 4 * g) & vmask;
-    u32x4 b = {__builtin_amdgcn_perm(c0, 0u, 0x0c050c04u), __builtin_amdgcn_perm(c0, 0u, 0x0c070c06u),
-               0u, 0u};
-    if (!HALF) {
-      const uint32_t c1 = *reinterpret_cast<const uint32_t*>(row + 16 + 4 * g) & vmask;
-      b[2] = __builtin_amdgcn_perm(c1, 0u, 0x0c050c04u);
-      b[3] = __builtin_amdgcn_perm(c1, 0u, 0x0c070c06u);
+    for (int j = 0; j < 8; ++j) pl[j] = (_Float16)__builtin_fmaf(pf[j], (float)vsc[j], -(float)pq[j]);
+    const half8 zv = as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]});
+    const half8 four = {4, 4, 4, 4, 4, 4, 4, 4};
+    // FOLD: 4 + zero * 4^k 2^-8 (exact for |zero| <= kFoldZeroMax);
+    // otherwise -zero * 4^k 2^-8 for the separate zero term (exact)
+    const half8 zt = FOLD ? __builtin_elementwise_fma(zv, half8(k4), four) : zv * half8(-k4);
+    const half8 off = FOLD ? zt : four;
+#pragma unroll
+    for (int blk = 2 * grp; blk < 2 * grp + 2; ++blk) {
+      const char* row = slot + kQsV + (4 * blk + (t >> 2)) * 32;
+      const uint32_t c0 = *reinterpret_cast<const uint32_t*>(row + 4 * g) & vmask;
+      const uint32_t c1 = HALF ? 0u : *reinterpret_cast<const uint32_t*>(row + 16 + 4 * g) & vmask;
+      const u32x4 bc = {codes_1024(c0, 0x00050004u), codes_1024(c0, 0x00070006u),
+                        codes_1024(c1, 0x00050004u), codes_1024(c1, 0x00070006u)};
+      const half8 r8 = {0.00390625f, 0.00390625f, 0.00390625f, 0.00390625f,
+                        0.00390625f, 0.00390625f, 0.00390625f, 0.00390625f};   // 2^-8
+      const half8 b = __builtin_elementwise_fma(as_h8(bc), r8, -off);
+      qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq, b, qs.O[blk], 0, 0, 0);
+      qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b, qs.O[blk], 0, 0, 0);
+      if (!FOLD) {
+        qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq, zt, qs.O[blk], 0, 0, 0);
+        qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, zt, qs.O[blk], 0, 0, 0);
+      }
     }
-    qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq[blk >> 1], as_h8(b), qs.O[blk], 0, 0, 0);
-    qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq[blk >> 1], as_h8(zz[blk >> 1]), qs.O[blk], 0, 0,
-                                                       0);
   }
 }
 
@@ -521,10 +550,21 @@ __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
   const half2v vs = __builtin_bit_cast(half2v, raw.vs);
   const float slack =
       __ballot(!(fmaxf((float)vs[0], (float)vs[1]) <= kSlackVScale)) ? 0.0f : kRescaleSlack;
-  if (xlim <= kTile / 2)
-    q_tile_body<MIXED, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
-  else
-    q_tile_body<MIXED, false>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+  // and two of its 128 V zeros
+  const half2v vz = __builtin_bit_cast(half2v, raw.vz);
+  const bool fold =
+      !__ballot(!(fmaxf(fabsf((float)vz[0]), fabsf((float)vz[1])) <= kFoldZeroMax));
+  if (fold) {
+    if (xlim <= kTile / 2)
+      q_tile_body<MIXED, true, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+    else
+      q_tile_body<MIXED, false, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+  } else {
+    if (xlim <= kTile / 2)
+      q_tile_body<MIXED, true, false>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+    else
+      q_tile_body<MIXED, false, false>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+  }
 }
 
 }  // namespace kvdec

@@ -162,6 +162,8 @@ def sparse_decode_attention_quantized(
     reference leaves undefined (quant_kernel.py:589-590), means the whole
     window stays fp16: k_cache / v_cache are [.., window, D_HEAD] (what
     build_quantized_kv_cache returns then) and there is no window-old part.
+    ``seq_len`` may also be a [BATCH] int32 tensor on the GPU: each sequence
+    is masked at its own length (ramp-up per sequence).
     """
     tensors = dict(zip(_KIVI_ORDER, (k_sink_packed, k_sink_scale, k_sink_zero,
                                      v_sink_packed, v_sink_scale, v_sink_zero,
@@ -172,7 +174,12 @@ def sparse_decode_attention_quantized(
     _checks.require_gpu_tensor("v_cache", v_cache, ndim=4)
     B, H, D = q.shape
     KVH = k_cache.shape[1]
-    window, sink, seq_len, R = int(window), int(sink), int(seq_len), int(residual_size)
+    varlen = isinstance(seq_len, torch.Tensor)
+    if varlen:
+        _checks.seq_lens_tensor("seq_len", seq_len, B, q.device)
+    else:
+        seq_len = int(seq_len)
+    window, sink, R = int(window), int(sink), int(residual_size)
     if window < 1:
         raise ValueError(f"window ({window}) must be >= 1")
     res_rows = min(window, R)
@@ -199,6 +206,12 @@ def sparse_decode_attention_quantized(
     if sm_scale is None:
         sm_scale = D_HEAD**-0.5
     arr = (K._vp * 12)(*[K.ptr(tensors[n]) if tensors[n].numel() else None for n in _KIVI_ORDER])
+    if varlen:
+        rc = K.lib.kvdec_sparse_decode_kivi_varlen(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), arr, K.ptr(o),
+                                                   K.ptr(seq_len), B, H, KVH, window, sink, R, G, bits,
+                                                   float(sm_scale), K.stream_of(q))
+        K.check(rc, "sparse_decode_attention_quantized")
+        return o
     ws, nbytes = K.workspace(K.KIND_KIVI, B, H, KVH, window, D, q.device)
     rc = K.lib.kvdec_sparse_decode_kivi(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), arr, K.ptr(o), B,
                                         H, KVH, seq_len, window, sink, R, G, bits, float(sm_scale),

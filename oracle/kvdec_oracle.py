@@ -508,6 +508,20 @@ def quantized_attention_masked(q, cache, seq_len, window, sm_scale, sink=4, resi
     return masked_attention(q, k, v, valid, sm_scale, dtype)
 
 
+def quantized_attention_varlen(q, cache, seq_lens, window, sm_scale, sink=4, residual_size=128,
+                               group_size=32, dtype=np.float64):
+    """quantized_attention_masked per sequence, at that sequence's length
+    (the reference's call at one scalar length, quant_kernel.py:551-581,
+    applied to each batch row)."""
+    q = np.asarray(q)
+    out = np.zeros(q.shape, dtype=dtype)
+    for b, n in enumerate(np.asarray(seq_lens).tolist()):
+        cb = {key: np.asarray(val)[b:b + 1] for key, val in cache.items()}
+        out[b] = quantized_attention_masked(q[b:b + 1], cb, n, window, sm_scale, sink, residual_size,
+                                            group_size, dtype)[0]
+    return out
+
+
 # --------------------------------------------------------------------------
 # Byte models (benchmark.py:30-31,56-57,121-129)
 # --------------------------------------------------------------------------

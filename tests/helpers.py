@@ -29,3 +29,16 @@ def max_abs(a, b):
 
 def randn(shape, seed, dtype=np.float32):
     return np.random.default_rng(seed).standard_normal(shape).astype(dtype)
+
+
+def assert_nearly_rounded(o, ref, slack=5e-5):
+    """Every fp16 output within half an fp16 ulp of the fp64 reference (what
+    one rounding of an exact result gives) plus `slack`: the kernel's own
+    arithmetic before that rounding must be far more accurate than fp16."""
+    o = np.asarray(o, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    half_ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
+    excess = np.abs(o - ref) - half_ulp
+    worst = np.unravel_index(np.argmax(excess), excess.shape)
+    assert excess[worst] <= slack, (f"output {o[worst]} vs reference {ref[worst]} at {worst}: "
+                                    f"{excess[worst]:.3g} beyond half an ulp")

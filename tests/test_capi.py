@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 16
+    assert len(funcs) == 17
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -154,6 +154,26 @@ def test_kivi_validation():
     assert _kivi(W=128 + 48) == E["GROUP"]                            # window-old not whole groups
     assert _kivi(seq_len=0) == E["SEQLEN"]
     assert _kivi(KVH=3) == E["SHAPE"]
+
+
+def _kivi_varlen(**kw):
+    a = dict(q=FAKE, kr=FAKE, vr=FAKE, o=FAKE, lens=FAKE, B=32, H=64, KVH=8, W=256, S=4, R=128,
+             group=32, bits=2, scale=0.088, stream=None)
+    a.update(kw)
+    arr = (K._vp * 12)(*([0x1000] * 12))
+    return K.lib.kvdec_sparse_decode_kivi_varlen(a["q"], a["kr"], a["vr"], arr, a["o"], a["lens"],
+                                                 a["B"], a["H"], a["KVH"], a["W"], a["S"], a["R"],
+                                                 a["group"], a["bits"], a["scale"], a["stream"])
+
+
+def test_kivi_varlen_validation():
+    assert _kivi_varlen(lens=None) == E["NULL"]
+    assert _kivi_varlen(q=None) == E["NULL"]
+    assert _kivi_varlen(bits=4) == E["BITS"]
+    assert _kivi_varlen(group=64) == E["UNSUPPORTED"]
+    assert _kivi_varlen(W=0) == E["WINDOW"]
+    assert _kivi_varlen(W=200) == E["GROUP"]
+    assert _kivi_varlen(H=60) == E["SHAPE"]
 
 
 def _quant(fn, **kw):

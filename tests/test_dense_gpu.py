@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from conftest import load_golden
-from helpers import ATTN_TOL, REF_TOL, SCALE, dev, host, max_abs, randn, say
+from helpers import ATTN_TOL, REF_TOL, SCALE, assert_nearly_rounded, dev, host, max_abs, randn, say
 from oracle import kvdec_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -38,7 +38,9 @@ def test_dense_lengths(L, device):
     say(f"dense B={B} L={L}")
     o = _run(q16, k16, v16, device)
     assert o.dtype == np.float16
-    assert max_abs(o, O.dense_attention(q16, k16, v16, SCALE)) < ATTN_TOL
+    ref = O.dense_attention(q16, k16, v16, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+    assert_nearly_rounded(o, ref)
     # the reference's own gate: fp16 kernel vs fp32 originals
     assert max_abs(o, O.dense_attention(q, k, v, SCALE, dtype=np.float32)) < REF_TOL
 
@@ -62,7 +64,30 @@ def test_dense_peaked_softmax(device):
     v16 = randn((B, KVH, L, D), 10, np.float16)
     say("dense peaked")
     o = _run(q16, k16, v16, device)
-    assert max_abs(o, O.dense_attention(q16, k16, v16, SCALE)) < ATTN_TOL
+    ref = O.dense_attention(q16, k16, v16, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+    assert_nearly_rounded(o, ref)
+
+
+@pytest.mark.parametrize("L", [40, 5000])
+def test_dense_dominant_token(L, device):
+    """One key aligned with the query carries ~99% of the weight: the output
+    is that token's V row, and an fp16 rounding of its probability would
+    show up whole.  Outputs within half an fp16 ulp of the fp64 oracle (plus
+    5e-5); V ~ N(0, 2) puts many outputs in [2, 8)."""
+    B, H, KVH, D = 3, 16, 2, 128
+    q16 = randn((B, H, D), 20, np.float16)
+    k = randn((B, KVH, L, D), 21)
+    for b in range(B):
+        for kv in range(KVH):
+            k[b, kv, (7 * b + kv) % L] = q16[b, kv * (H // KVH)] * 0.9
+    k16 = k.astype(np.float16)
+    v16 = (randn((B, KVH, L, D), 22) * 2).astype(np.float16)
+    say(f"dense dominant L={L}")
+    o = _run(q16, k16, v16, device)
+    ref = O.dense_attention(q16, k16, v16, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+    assert_nearly_rounded(o, ref)
 
 
 def test_dense_long_context_large_offsets(device):

@@ -190,6 +190,23 @@ def test_sparse_varlen_is_per_sequence_call():
     np.testing.assert_allclose(got[0], np.repeat(vc[0, :, 0], H // KVH, axis=0), rtol=1e-12)
 
 
+def test_quantized_varlen_rows_are_independent():
+    """Equal lengths give the batched call; each row at its own length is
+    that row of the batched call at that length."""
+    r = _rng(14)
+    B, H, KVH, D, W, S = 3, 4, 2, 64, 160, 4
+    kc = r.standard_normal((B, KVH, S + W, D)).astype(np.float16)
+    vc = r.standard_normal((B, KVH, S + W, D)).astype(np.float16)
+    cache = O.build_quantized_kv_cache(kc, vc)
+    q = r.standard_normal((B, H, D)).astype(np.float16)
+    same = O.quantized_attention_varlen(q, cache, [500] * B, W, 0.3)
+    np.testing.assert_array_equal(same, O.quantized_attention_masked(q, cache, 500, W, 0.3))
+    lens = [2, 100, 500]
+    got = O.quantized_attention_varlen(q, cache, lens, W, 0.3)
+    for b, n in enumerate(lens):
+        np.testing.assert_array_equal(got[b], O.quantized_attention_masked(q, cache, n, W, 0.3)[b])
+
+
 # ----------------------------------------------------------------------------
 # StreamingLLM sink + window
 # ----------------------------------------------------------------------------

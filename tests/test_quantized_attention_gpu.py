@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from conftest import load_golden
-from helpers import ATTN_TOL, REF_TOL, SCALE, dev, host, max_abs, randn, say
+from helpers import ATTN_TOL, REF_TOL, SCALE, assert_nearly_rounded, dev, host, max_abs, randn, say
 from oracle import kvdec_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -110,6 +110,58 @@ def test_quantized_attention_growing_logits(vmul, device):
     ref = O.quantized_attention(host(q), W - R, _host_cache(cache), SCALE)
     assert np.all(np.isfinite(o))
     assert max_abs(o, ref) < ATTN_TOL * vmul
+    assert_nearly_rounded(o, ref, 5e-5 * vmul)
+
+
+def test_quantized_attention_large_v_offsets(device):
+    """V rows far from zero relative to their spread (100 + 0.05 N(0,1)):
+    zero points beyond 1000, which take the separate zero-term path, in
+    some groups and tiles next to ordinary ones.  Outputs near 100 are
+    checked to half an fp16 ulp."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D, W = 2, 16, 2, 128, 512
+    gen = torch.Generator(device=device).manual_seed(17)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device).half()
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device)
+    far = torch.zeros(S + W, dtype=torch.bool, device=device)
+    far[S + 32:S + 96] = True                   # two whole window-old tiles
+    far[S + 200:S + 210] = True                 # part of a tile
+    vc[:, :, far] = 100 + 0.05 * vc[:, :, far]
+    vc[:, :, :, 64:] = torch.where(far[None, None, :, None], vc[:, :, :, 64:] - 100, vc[:, :, :, 64:])
+    vc = vc.half()
+    say("kivi large V offsets")
+    cache = build_quantized_kv_cache(kc, vc)
+    zeros = host(cache["v_win_zero"]).astype(np.float32)
+    assert np.abs(zeros).max() > 1000 and (np.abs(zeros) <= 3).any()
+    o = _attend(q, cache, 163840, W)
+    ref = O.quantized_attention(host(q), W - R, _host_cache(cache), SCALE)
+    assert_nearly_rounded(o, ref)
+
+
+@pytest.mark.parametrize("where", ["window_old", "sink", "residual"])
+def test_quantized_attention_dominant_token(where, device):
+    """One token carries almost all of a head's softmax weight, so the output
+    is (nearly) that token's V row: an fp16 rounding of its probability (or
+    of probability x V scale) would show up whole in the output.  Every
+    output must be within half an fp16 ulp of the fp64 oracle (plus 5e-5)."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D, W = 4, 32, 4, 128, 1024
+    gen = torch.Generator(device=device).manual_seed(5)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device)
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device) * 1.9
+    slot = {"window_old": S + 300, "sink": 2, "residual": S + W - 5}[where]
+    G = H // KVH
+    for kv in range(KVH):                      # query head kv * G of every KV head
+        kc[:, kv, slot] = q[:, kv * G].float() * 0.9
+    kc, vc = kc.half(), vc.half()
+    say(f"kivi dominant token in {where}")
+    cache = build_quantized_kv_cache(kc, vc)
+    o = _attend(q, cache, 163840, W)
+    ref = O.quantized_attention(host(q), W - R, _host_cache(cache), SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+    assert_nearly_rounded(o, ref)
 
 
 @pytest.mark.parametrize("L", [1, 3, 4, 5, 60, 200, 300, 387, 388, 389])
@@ -130,6 +182,33 @@ def test_quantized_attention_rampup(L, device):
     o = _attend(dev(q16, device), cache, L, W)
     ref = O.quantized_attention_masked(q16, _host_cache(cache), L, W, SCALE)
     assert max_abs(o, ref) < ATTN_TOL
+
+
+@pytest.mark.parametrize("W", [96, 384])
+def test_quantized_attention_varlen(W, device):
+    """One length per sequence: pre-sink, ramp-up (fp16 residual slots,
+    then window-old slots partly unwritten), the last ramp-up length and
+    steady state share one launch; each row matches the oracle at its own
+    length and the scalar-length call at that length."""
+    from quant_kernel import build_quantized_kv_cache
+    lens = [1, 3, 60, 200, S + W - 1, S + W, 163840]
+    B, H, KVH, D = len(lens), 16, 2, 128
+    kc = np.zeros((B, KVH, S + W, D), np.float32)
+    vc = np.zeros((B, KVH, S + W, D), np.float32)
+    for b, n in enumerate(lens):
+        m = min(n, S + W + 64)
+        kb, vb = O.build_compacted_cache(randn((1, KVH, m, D), 60 + b), randn((1, KVH, m, D), 70 + b),
+                                         min(n, m), W, S, garbage=3.0)
+        kc[b], vc[b] = kb[0], vb[0]
+    q16 = randn((B, H, D), 80 + W, np.float16)
+    say(f"kivi varlen W={W}")
+    cache = build_quantized_kv_cache(dev(kc.astype(np.float16), device), dev(vc.astype(np.float16), device))
+    o = _attend(dev(q16, device), cache, torch.tensor(lens, dtype=torch.int32, device=device), W)
+    ref = O.quantized_attention_varlen(q16, _host_cache(cache), lens, W, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+    qd = dev(q16, device)
+    for b, n in enumerate(lens):
+        assert max_abs(o[b], _attend(qd, cache, n, W)[b]) < ATTN_TOL, n
 
 
 @pytest.mark.parametrize("W", [32, 48, 96])
