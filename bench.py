@@ -18,7 +18,8 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
   stream    a decode loop on the streaming KIVI cache (kivi_stream.py, W=256):
             reserve the next token's ring row (quantizing a block every 32
             steps), then attend; each cache advances 32 steps, so the time
-            includes one eviction per 32 steps
+            includes one eviction per 32 steps.  Also the same loop with one
+            ring state per sequence (KiviStreamBatch: + the bookkeeping launch)
   paged     the dense L=163840 cache scattered over 16-token pages in a
             random order (vLLM's [pages, 16, KVH, D] layout), decoded through
             block tables and per-sequence lengths (paged_kernel.py)
@@ -358,7 +359,26 @@ def main():
 
         ms, _ = graph_time(scall, ns, ssteps, Wu)
         out["kivi_stream_w256"] = path_record(ms, bytes_stream_step(W), ns, ssteps)
-        del caches, toks
+        del caches
+
+        # the same loop with one ring state per sequence (kivi_stream.
+        # KiviStreamBatch): per step the on-GPU bookkeeping launch, the
+        # evictions and the decode, every sequence active
+        from kivi_stream import KiviStreamBatch
+        batches = []
+        for _ in range(ns):
+            kc, vc = compacted(W)
+            batches.append(KiviStreamBatch.from_prefill(kc, vc, W))
+            del kc, vc
+
+        def bcall(i):
+            c = batches[i % ns]
+            c.reserve()
+            return c.attend(toks[i % ns][0])
+
+        ms, _ = graph_time(bcall, ns, ssteps, Wu)
+        out["kivi_stream_seqs_w256"] = path_record(ms, bytes_stream_step(W), ns, ssteps)
+        del batches, toks
 
     if "sparse" in paths:
         ns = n_sets(bytes_sparse(W))

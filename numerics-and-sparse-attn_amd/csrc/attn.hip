@@ -484,10 +484,16 @@ struct PagedSrc {
 };
 
 // KIVI cache: the fp16 residual (slots sink + win_tok ..) and the quantized
-// sink and window-old groups.  VARLEN: each sequence's slot validity comes
-// from its own length lens[b] instead of P.R (a separate instantiation, so
-// the one-length kernel carries none of it).
-template <bool VARLEN>
+// sink and window-old groups.  Slot validity per MODE (separate
+// instantiations, so the one-length kernel carries nothing of the others):
+//   kOneRange  P.R for every sequence
+//   kSeqLens   the _kv_indices rule at each sequence's own length lens[b]
+//   kSeqRings  the residual is a ring of res_rows rows whose valid rows are
+//              [start, start + count) mod res_rows, ring[b] = {start, count}
+//              (a decode-time cache; every sink and window-old slot valid)
+enum { kOneRange = 0, kSeqLens = 1, kSeqRings = 2 };
+
+template <int MODE>
 struct KiviSrcBase {
   const _Float16* kres;
   const _Float16* vres;
@@ -497,7 +503,7 @@ struct KiviSrcBase {
   int sink;
   int win_tok;     // window - residual
   int nwt;         // win_tok / 32
-  const int32_t* lens;   // VARLEN: per-sequence lengths [B]
+  const int32_t* lens;   // kSeqLens: per-sequence lengths [B]; kSeqRings: {start, count} [B][2]
   int window;
 
   // Work split.  While the residual has at most kWaves tiles, the first nrw
@@ -527,8 +533,16 @@ struct KiviSrcBase {
                                           int lane, int* ctr, Sync&& sync, WaveState& st) const {
     const int nrw = n_res_waves();
     SlotRanges R = P.R;
-    if constexpr (VARLEN)
+    if constexpr (MODE == kSeqLens) {
       R = sparse_ranges(max((int)((cint32*)lens)[pair / P.KVH], 0), window, sink, KVDEC_LAYOUT_LINEAR);
+    } else if constexpr (MODE == kSeqRings) {
+      const int64_t b = pair / P.KVH;
+      const int start = min(max((int)((cint32*)lens)[2 * b], 0), res_rows - 1);
+      const int count = min(max((int)((cint32*)lens)[2 * b + 1], 0), res_rows);
+      const int base = sink + win_tok, end = start + count;
+      R = end <= res_rows ? SlotRanges{base, base + start, base + end}
+                          : SlotRanges{base + end - res_rows, base + start, base + res_rows};
+    }
     QRegion S = sinkq, Wq = winq;
     S.kp += (size_t)pair * 8 * kHeadDim;
     S.ks += (size_t)pair * kHeadDim;
@@ -589,7 +603,7 @@ struct KiviSrcBase {
         const int qe = nqw + rw;
         qonly.load(qe, E, lane);
         sync(c, true);
-        if constexpr (VARLEN) c.R = R;
+        if constexpr (MODE != kOneRange) c.R = R;
         F16Raw X;
         rit.load(rw, X, lane);
         if (qe < qonly.n) {
@@ -601,7 +615,7 @@ struct KiviSrcBase {
         Ring<F16Items> rring;
         ring_begin(rit, rring, rw, rw + nrw, lane);
         sync(c, dyn);
-        if constexpr (VARLEN) c.R = R;
+        if constexpr (MODE != kOneRange) c.R = R;
         if (rit.n > 2 * nrw)
           ring_run_dynamic(rit, rring, ctr, st, c);
         else
@@ -624,7 +638,7 @@ struct KiviSrcBase {
       Ring<QItems<false>> qring;
       ring_begin(qonly, qring, qw, qw + nqw + nrw, lane);
       sync(c, dyn || nqw > 0);
-      if constexpr (VARLEN) c.R = R;
+      if constexpr (MODE != kOneRange) c.R = R;
       if (dyn_q)
         ring_run_dynamic(qonly, qring, ctr + 1, qref, c);
       else
@@ -635,8 +649,9 @@ struct KiviSrcBase {
   }
 };
 
-struct KiviSrc : KiviSrcBase<false> {};
-struct KiviVarSrc : KiviSrcBase<true> {};
+struct KiviSrc : KiviSrcBase<kOneRange> {};
+struct KiviVarSrc : KiviSrcBase<kSeqLens> {};
+struct KiviRingSrc : KiviSrcBase<kSeqRings> {};
 
 template <class Src>
 __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) {
@@ -856,6 +871,73 @@ int kivi_decode(const void* q, const void* k_res, const void* v_res, const void*
   return launch_attn(P, S1, true, 0, st);
 }
 
+// The fused decode over a decode-time KIVI cache: one ring state for every
+// sequence (ring null: ring_start / ring_count) or one per sequence.
+int stream_decode(const void* q, const void* k_ring, const void* v_ring, const void* const* kivi,
+                  void* o, const int32_t* ring, int64_t B, int32_t H, int32_t KVH, int32_t sink,
+                  int32_t n_groups, int32_t ring_cap, int32_t ring_start, int32_t ring_count,
+                  int32_t group, int32_t bits, float sm_scale, void* stream) {
+  if (!q || !k_ring || !v_ring || !kivi || !o) return KVDEC_E_NULL;
+  if (bits != 2) return KVDEC_E_BITS;
+  if (group != 32) return KVDEC_E_UNSUPPORTED;
+  int rc = check_heads(B, H, KVH, kHeadDim);
+  if (rc) return rc;
+  if (sink < 1 || sink > group || n_groups < 0) return KVDEC_E_WINDOW;
+  if (ring_cap < 2 * kTile || ring_cap % kTile != 0) return KVDEC_E_WINDOW;
+  for (int i = 0; i < 6; ++i)
+    if (!kivi[i]) return KVDEC_E_NULL;
+  if (n_groups > 0)
+    for (int i = 6; i < 12; ++i)
+      if (!kivi[i]) return KVDEC_E_NULL;
+  const int64_t win_tok = (int64_t)n_groups * group;
+  if ((int64_t)ring_cap * kRowBytes >= ((int64_t)1 << 31) || win_tok * kHeadDim >= ((int64_t)1 << 31))
+    return KVDEC_E_SHAPE;
+
+  AttnCommon P{};
+  P.q = static_cast<const _Float16*>(q);
+  P.o = static_cast<_Float16*>(o);
+  P.ws = nullptr;
+  P.pairs = B * KVH;
+  P.H = H;
+  P.KVH = KVH;
+  P.G = H / KVH;
+  P.n_tiles = (int)(1 + n_groups + ring_cap / kTile);
+  P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
+  // every sink and window-old slot is valid; ring rows [start, start + count)
+  // (mod cap) of the residual are, at slots base + row
+  const int base = sink + (int)win_tok;
+  const int end = ring_start + ring_count;
+  if (end <= ring_cap)
+    P.R = SlotRanges{base, base + ring_start, base + end};
+  else
+    P.R = SlotRanges{base + end - ring_cap, base + ring_start, base + ring_cap};
+
+  auto u8 = [&](int i) { return static_cast<const uint8_t*>(kivi[i]); };
+  auto f16 = [&](int i) { return static_cast<const _Float16*>(kivi[i]); };
+  KiviRingSrc S{};
+  S.kres = static_cast<const _Float16*>(k_ring);
+  S.vres = static_cast<const _Float16*>(v_ring);
+  S.res_rows = ring_cap;
+  S.sinkq = QRegion{u8(0), f16(1), f16(2), u8(3), f16(4), f16(5)};
+  S.winq = n_groups > 0 ? QRegion{u8(6), f16(7), f16(8), u8(9), f16(10), f16(11)} : S.sinkq;
+  S.sink = sink;
+  S.win_tok = (int)win_tok;
+  S.nwt = n_groups;
+  S.lens = ring;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (ring) return launch_attn(P, S, true, 0, st);
+  KiviSrc S1{};
+  S1.kres = S.kres;
+  S1.vres = S.vres;
+  S1.res_rows = S.res_rows;
+  S1.sinkq = S.sinkq;
+  S1.winq = S.winq;
+  S1.sink = S.sink;
+  S1.win_tok = S.win_tok;
+  S1.nwt = S.nwt;
+  return launch_attn(P, S1, true, 0, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1061,55 +1143,20 @@ int kvdec_kivi_stream_decode(const void* q, const void* k_ring, const void* v_ri
                              int32_t sink, int32_t n_groups, int32_t ring_cap, int32_t ring_start,
                              int32_t ring_count, int32_t group, int32_t bits, float sm_scale,
                              void* stream) {
-  if (!q || !k_ring || !v_ring || !kivi || !o) return KVDEC_E_NULL;
-  if (bits != 2) return KVDEC_E_BITS;
-  if (group != 32) return KVDEC_E_UNSUPPORTED;
-  int rc = check_heads(B, H, KVH, kHeadDim);
-  if (rc) return rc;
-  if (sink < 1 || sink > group || n_groups < 0) return KVDEC_E_WINDOW;
-  if (ring_cap < 2 * kTile || ring_cap % kTile != 0) return KVDEC_E_WINDOW;
   if (ring_start < 0 || ring_start >= ring_cap || ring_count < 1 || ring_count > ring_cap)
     return KVDEC_E_WINDOW;
-  for (int i = 0; i < 6; ++i)
-    if (!kivi[i]) return KVDEC_E_NULL;
-  if (n_groups > 0)
-    for (int i = 6; i < 12; ++i)
-      if (!kivi[i]) return KVDEC_E_NULL;
-  const int64_t win_tok = (int64_t)n_groups * group;
-  if ((int64_t)ring_cap * kRowBytes >= ((int64_t)1 << 31) || win_tok * kHeadDim >= ((int64_t)1 << 31))
-    return KVDEC_E_SHAPE;
+  return stream_decode(q, k_ring, v_ring, kivi, o, nullptr, B, H, KVH, sink, n_groups, ring_cap,
+                       ring_start, ring_count, group, bits, sm_scale, stream);
+}
 
-  AttnCommon P{};
-  P.q = static_cast<const _Float16*>(q);
-  P.o = static_cast<_Float16*>(o);
-  P.ws = nullptr;
-  P.pairs = B * KVH;
-  P.H = H;
-  P.KVH = KVH;
-  P.G = H / KVH;
-  P.n_tiles = (int)(1 + n_groups + ring_cap / kTile);
-  P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
-  // every sink and window-old slot is valid; ring rows [start, start + count)
-  // (mod cap) of the residual are, at slots base + row
-  const int base = sink + (int)win_tok;
-  const int end = ring_start + ring_count;
-  if (end <= ring_cap)
-    P.R = SlotRanges{base, base + ring_start, base + end};
-  else
-    P.R = SlotRanges{base + end - ring_cap, base + ring_start, base + ring_cap};
-
-  auto u8 = [&](int i) { return static_cast<const uint8_t*>(kivi[i]); };
-  auto f16 = [&](int i) { return static_cast<const _Float16*>(kivi[i]); };
-  KiviSrc S{};
-  S.kres = static_cast<const _Float16*>(k_ring);
-  S.vres = static_cast<const _Float16*>(v_ring);
-  S.res_rows = ring_cap;
-  S.sinkq = QRegion{u8(0), f16(1), f16(2), u8(3), f16(4), f16(5)};
-  S.winq = n_groups > 0 ? QRegion{u8(6), f16(7), f16(8), u8(9), f16(10), f16(11)} : S.sinkq;
-  S.sink = sink;
-  S.win_tok = (int)win_tok;
-  S.nwt = n_groups;
-  return launch_attn(P, S, true, 0, static_cast<hipStream_t>(stream));
+int kvdec_kivi_stream_decode_seqs(const void* q, const void* k_ring, const void* v_ring,
+                                  const void* const* kivi, void* o, const int32_t* ring,
+                                  int64_t B, int32_t H, int32_t KVH, int32_t sink,
+                                  int32_t n_groups, int32_t ring_cap, int32_t group, int32_t bits,
+                                  float sm_scale, void* stream) {
+  if (!ring) return KVDEC_E_NULL;
+  return stream_decode(q, k_ring, v_ring, kivi, o, ring, B, H, KVH, sink, n_groups, ring_cap, 0,
+                       ring_cap, group, bits, sm_scale, stream);
 }
 
 }  // extern "C"

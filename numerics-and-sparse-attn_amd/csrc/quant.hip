@@ -464,20 +464,34 @@ struct StreamArgs {
   uint8_t* vp;             // [pairs][nwg * group][D / 4]
   _Float16* vs;            // [pairs][nwg * group][D / group]
   _Float16* vz;
-  int D, cap, row, blk, slot, nwg;
+  const int32_t* plan;     // per sequence {row, evict block, evict slot} [B][3], or null
+  int D, cap, row, blk, slot, nwg, KVH;
 };
 
 __global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
   const int64_t pair = blockIdx.x;
   const int D = a.D;
-  if (a.k_new)
+  int row = a.row, blk = a.blk, slot = a.slot;
+  if (a.plan) {
+    // this sequence's step; entries outside the ring mean "no write" /
+    // "no eviction" (the plan is device data the host did not check)
+    const int32_t* pb = a.plan + 3 * (pair / a.KVH);
+    row = pb[0];
+    blk = pb[1];
+    slot = pb[2];
+    if (row < 0 || row >= a.cap) row = -1;
+    if (blk < 0 || blk >= a.cap / kGroup || a.nwg <= 0 || slot < 0 || slot >= a.nwg ||
+        (row >= 0 && row / kGroup == blk))
+      blk = -1;
+  }
+  if (a.k_new && row >= 0)
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
-      a.k_ring[((size_t)pair * a.cap + a.row) * D + i] = a.k_new[(size_t)pair * D + i];
-      a.v_ring[((size_t)pair * a.cap + a.row) * D + i] = a.v_new[(size_t)pair * D + i];
+      a.k_ring[((size_t)pair * a.cap + row) * D + i] = a.k_new[(size_t)pair * D + i];
+      a.v_ring[((size_t)pair * a.cap + row) * D + i] = a.v_new[(size_t)pair * D + i];
     }
-  if (a.blk < 0) return;
-  const size_t blk0 = (size_t)pair * a.cap + (size_t)a.blk * kGroup;   // first ring row of the block
-  const size_t g = (size_t)pair * a.nwg + a.slot;
+  if (blk < 0) return;
+  const size_t blk0 = (size_t)pair * a.cap + (size_t)blk * kGroup;   // first ring row of the block
+  const size_t g = (size_t)pair * a.nwg + slot;
   // K: one thread per channel, its 32 tokens (per-channel group)
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float x[kGroup];
@@ -505,6 +519,45 @@ __global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
     a.vs[tok * ng + cg] = (_Float16)q.s;
     a.vz[tok * ng + cg] = (_Float16)q.z;
   }
+}
+
+// Per-sequence ring bookkeeping of a decode-time KIVI cache, one thread per
+// sequence.  appended[b] counts the tokens appended since sequence b's
+// prefill; the state after n appends is fixed by n: n / 32 evictions, so the
+// residual ring holds rows [start, start + count) mod cap with
+// start = 32 (n / 32) mod cap and count = residual + n mod 32, and the
+// oldest window-old group sits in slot (n / 32) mod n_groups.  An active
+// sequence takes row (start + count) mod cap; when that fills the ring its
+// oldest 32-row block is quantized into the oldest group's slot.  Writes
+// plan[b] = {row, evict block, evict slot} (-1: none) and ring[b] =
+// {start, count} after the step, and advances appended[b].
+__global__ __launch_bounds__(256) void stream_plan_kernel(int32_t* appended, const int32_t* active,
+                                                          int32_t* plan, int32_t* ring, int64_t B,
+                                                          int residual, int cap, int ngroups) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int n = max(appended[b], 0);
+  const int e = n / kGroup;
+  int start = (int)(((int64_t)kGroup * e) % cap);
+  int count = residual + n % kGroup;
+  int32_t p0 = -1, p1 = -1, p2 = -1;
+  if (!active || active[b]) {
+    p0 = (start + count) % cap;
+    if (count + 1 == cap) {            // the ring is full: evict its oldest block
+      p1 = start / kGroup;
+      p2 = ngroups > 0 ? e % ngroups : -1;
+      start = (start + kGroup) % cap;
+      count = residual;
+    } else {
+      count += 1;
+    }
+    appended[b] = n + 1;
+  }
+  plan[3 * b] = p0;
+  plan[3 * b + 1] = p1;
+  plan[3 * b + 2] = p2;
+  ring[2 * b] = start;
+  ring[2 * b + 1] = count;
 }
 
 // ---------------------------------------------------------------------------
@@ -711,6 +764,59 @@ int kvdec_kivi_stream_append(const void* k_new, const void* v_new, void* k_ring,
   a.slot = evict_slot;
   a.nwg = n_groups;
   if (a.blk >= 0) {
+    a.kp = static_cast<uint8_t*>(win[0]);
+    a.ks = static_cast<_Float16*>(win[1]);
+    a.kz = static_cast<_Float16*>(win[2]);
+    a.vp = static_cast<uint8_t*>(win[3]);
+    a.vs = static_cast<_Float16*>(win[4]);
+    a.vz = static_cast<_Float16*>(win[5]);
+  }
+  hipLaunchKernelGGL(stream_append_kernel, dim3((unsigned)(B * KVH)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status();
+}
+
+int kvdec_kivi_stream_plan(int32_t* appended, const int32_t* active, int32_t* plan,
+                           int32_t* ring, int64_t B, int32_t residual, int32_t ring_cap,
+                           int32_t n_groups, int32_t group, void* stream) {
+  if (!appended || !plan || !ring) return KVDEC_E_NULL;
+  if (group != kGroup) return KVDEC_E_UNSUPPORTED;
+  if (B < 1 || n_groups < 0) return KVDEC_E_SHAPE;
+  if (residual < kGroup || residual % kGroup != 0 || ring_cap != residual + kGroup)
+    return KVDEC_E_WINDOW;
+  hipLaunchKernelGGL(stream_plan_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), appended, active, plan, ring, B, residual,
+                     ring_cap, n_groups);
+  return launch_status();
+}
+
+int kvdec_kivi_stream_append_seqs(const void* k_new, const void* v_new, void* k_ring, void* v_ring,
+                                  void* const* win, int64_t B, int32_t KVH, int32_t D,
+                                  int32_t ring_cap, int32_t n_groups, const int32_t* plan,
+                                  int32_t group, int32_t bits, void* stream) {
+  if (!k_ring || !v_ring || !plan || (!k_new) != (!v_new)) return KVDEC_E_NULL;
+  if (bits != 2) return KVDEC_E_BITS;
+  if (group != kGroup) return KVDEC_E_UNSUPPORTED;
+  if (B < 1 || KVH < 1 || D < 1 || B * (int64_t)KVH > 0x7fffffffLL) return KVDEC_E_SHAPE;
+  if (D % kGroup != 0) return KVDEC_E_DGROUP;
+  if (ring_cap < 2 * kGroup || ring_cap % kGroup != 0) return KVDEC_E_WINDOW;
+  if (n_groups < 0) return KVDEC_E_SHAPE;
+  if (n_groups > 0) {
+    if (!win) return KVDEC_E_NULL;
+    for (int i = 0; i < 6; ++i)
+      if (!win[i]) return KVDEC_E_NULL;
+  }
+  StreamArgs a{};
+  a.k_new = static_cast<const _Float16*>(k_new);
+  a.v_new = static_cast<const _Float16*>(v_new);
+  a.k_ring = static_cast<_Float16*>(k_ring);
+  a.v_ring = static_cast<_Float16*>(v_ring);
+  a.plan = plan;
+  a.D = D;
+  a.cap = ring_cap;
+  a.nwg = n_groups;
+  a.KVH = KVH;
+  if (n_groups > 0) {
     a.kp = static_cast<uint8_t*>(win[0]);
     a.ks = static_cast<_Float16*>(win[1]);
     a.kz = static_cast<_Float16*>(win[2]);

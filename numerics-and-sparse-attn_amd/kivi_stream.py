@@ -71,6 +71,42 @@ class RingState:
         return row, evict_block, evict_slot
 
 
+def _prefill_state(k, v, window, sink, residual_size):
+    """The quantized sink group, the window-old groups and the residual ring
+    (rows 0 .. residual - 1 = the last residual prefill tokens) of a
+    [B, KVH, L, D] fp16 prefill."""
+    _checks.require_gpu_tensor("k", k, ndim=4, contiguous=False)   # sliced, then copied
+    _checks.require_gpu_tensor("v", v, ndim=4, contiguous=False)
+    _checks.require_same_device(("k", k), ("v", v))
+    B, KVH, L, D = k.shape
+    _checks.require_shape("v", v, (B, KVH, L, D))
+    R, G = int(residual_size), GROUP_SIZE
+    window, sink = int(window), int(sink)
+    if window < R or (window - R) % G or R % G or not 1 <= sink <= G:
+        raise ValueError(f"unsupported window={window} / residual={R} / sink={sink}")
+    if L < sink + window:
+        raise ValueError(f"prefill length {L} < sink + window = {sink + window}")
+    pad = G - sink
+    t = {}
+
+    def padded(x):
+        real = x[:, :, :sink]
+        return torch.cat([real, real[:, :, :1].expand(-1, -1, pad, -1)], dim=2).contiguous()
+
+    t["k_sink_packed"], t["k_sink_scale"], t["k_sink_zero"] = quantize_k_cache(padded(k))
+    t["v_sink_packed"], t["v_sink_scale"], t["v_sink_zero"] = quantize_v_cache(padded(v))
+    win = k[:, :, L - window:L - R].contiguous()
+    t["k_win_packed"], t["k_win_scale"], t["k_win_zero"] = quantize_k_cache(win)
+    win = v[:, :, L - window:L - R].contiguous()
+    t["v_win_packed"], t["v_win_scale"], t["v_win_zero"] = quantize_v_cache(win)
+    cap = R + G
+    t["k_ring"] = torch.empty(B, KVH, cap, D, dtype=torch.float16, device=k.device)
+    t["v_ring"] = torch.empty(B, KVH, cap, D, dtype=torch.float16, device=k.device)
+    t["k_ring"][:, :, :R] = k[:, :, L - R:]
+    t["v_ring"][:, :, :R] = v[:, :, L - R:]
+    return t
+
+
 class KiviStreamCache:
     """Streaming KIVI cache of B sequences that advance together (one scalar
     length, as in the reference's decode calls)."""
@@ -86,37 +122,10 @@ class KiviStreamCache:
     def from_prefill(cls, k, v, window, sink=SINK_SIZE, residual_size=RESIDUAL_SIZE):
         """k, v: [B, KVH, L, D] fp16 of positions 0..L-1 (a prefill), with
         L >= sink + window (steady state: every window slot is filled)."""
-        _checks.require_gpu_tensor("k", k, ndim=4, contiguous=False)   # sliced, then copied
-        _checks.require_gpu_tensor("v", v, ndim=4, contiguous=False)
-        _checks.require_same_device(("k", k), ("v", v))
-        B, KVH, L, D = k.shape
-        _checks.require_shape("v", v, (B, KVH, L, D))
+        t = _prefill_state(k, v, window, sink, residual_size)
         R, G = int(residual_size), GROUP_SIZE
-        window, sink = int(window), int(sink)
-        if window < R or (window - R) % G or R % G or not 1 <= sink <= G:
-            raise ValueError(f"unsupported window={window} / residual={R} / sink={sink}")
-        if L < sink + window:
-            raise ValueError(f"prefill length {L} < sink + window = {sink + window}")
-        pad = G - sink
-        t = {}
-
-        def padded(x):
-            real = x[:, :, :sink]
-            return torch.cat([real, real[:, :, :1].expand(-1, -1, pad, -1)], dim=2).contiguous()
-
-        t["k_sink_packed"], t["k_sink_scale"], t["k_sink_zero"] = quantize_k_cache(padded(k))
-        t["v_sink_packed"], t["v_sink_scale"], t["v_sink_zero"] = quantize_v_cache(padded(v))
-        win = k[:, :, L - window:L - R].contiguous()
-        t["k_win_packed"], t["k_win_scale"], t["k_win_zero"] = quantize_k_cache(win)
-        win = v[:, :, L - window:L - R].contiguous()
-        t["v_win_packed"], t["v_win_scale"], t["v_win_zero"] = quantize_v_cache(win)
-        cap = R + G
-        t["k_ring"] = torch.empty(B, KVH, cap, D, dtype=torch.float16, device=k.device)
-        t["v_ring"] = torch.empty(B, KVH, cap, D, dtype=torch.float16, device=k.device)
-        t["k_ring"][:, :, :R] = k[:, :, L - R:]
-        t["v_ring"][:, :, :R] = v[:, :, L - R:]
-        ring = RingState(cap=cap, residual=R, n_groups=(window - R) // G, count=R)
-        return cls(t, ring, L, window, sink)
+        ring = RingState(cap=R + G, residual=R, n_groups=(int(window) - R) // G, count=R)
+        return cls(t, ring, k.shape[2], int(window), int(sink))
 
     @property
     def shape(self):
@@ -188,3 +197,114 @@ class KiviStreamCache:
         """Valid residual ring rows from the oldest token to the newest."""
         r = self.ring
         return [(r.start + i) % r.cap for i in range(r.count)]
+
+
+class KiviStreamBatch:
+    """Decode-time KIVI cache whose B sequences keep separate ring states,
+    for continuous batching: a sequence can take a new prefill in its batch
+    slot (admit) and sit out steps (the `active` mask), while the others go
+    on.  The bookkeeping lives on the GPU (kvdec_kivi_stream_plan: a token
+    count per sequence, from which each step's ring row, eviction and ring
+    state follow), so a step is three launches and no host round trip:
+    plan, append (quantize-on-evict), attend.  Each sequence's state equals
+    a KiviStreamCache of that sequence alone after the same appends."""
+
+    def __init__(self, tensors, window, sink, residual):
+        self.t = tensors
+        self.window, self.sink, self.residual = int(window), int(sink), int(residual)
+        self.cap = self.residual + GROUP_SIZE
+        self.n_groups = (self.window - self.residual) // GROUP_SIZE
+        B = tensors["k_ring"].shape[0]
+        dev = tensors["k_ring"].device
+        self.appended = torch.zeros(B, dtype=torch.int32, device=dev)   # tokens since each prefill
+        self.plan = torch.full((B, 3), -1, dtype=torch.int32, device=dev)
+        self.ring = torch.tensor([[0, self.residual]] * B, dtype=torch.int32, device=dev)
+
+    @classmethod
+    def from_prefill(cls, k, v, window, sink=SINK_SIZE, residual_size=RESIDUAL_SIZE):
+        """k, v: [B, KVH, L, D] fp16 prefills of one length L >= sink + window
+        (sequences of other lengths join with admit())."""
+        return cls(_prefill_state(k, v, window, sink, residual_size), window, sink, residual_size)
+
+    @property
+    def shape(self):
+        B, KVH, cap, D = self.t["k_ring"].shape
+        return B, KVH, D
+
+    def admit(self, b, k, v):
+        """Start sequence slot b over from a prefill k, v [KVH, L, D] fp16
+        (L >= sink + window); the other slots are untouched.  Ordered on
+        torch's current stream like every other call."""
+        B, KVH, D = self.shape
+        if not 0 <= int(b) < B:
+            raise ValueError(f"slot {b} outside the batch of {B}")
+        one = _prefill_state(k[None], v[None], self.window, self.sink, self.residual)
+        for name, x in one.items():
+            self.t[name][b] = x[0]
+        self.appended[b] = 0
+        self.ring[b, 0] = 0
+        self.ring[b, 1] = self.residual
+
+    def _plan(self, active):
+        B, KVH, D = self.shape
+        act = None
+        if active is not None:
+            act = active.to(device=self.appended.device, dtype=torch.int32).contiguous()
+            _checks.require_gpu_tensor("active", act, dtypes=(torch.int32,), ndim=1)
+            _checks.require_shape("active", act, (B,))
+        rc = K.lib.kvdec_kivi_stream_plan(K.ptr(self.appended), K.ptr(act) if act is not None else None,
+                                          K.ptr(self.plan), K.ptr(self.ring), B, self.residual, self.cap,
+                                          self.n_groups, GROUP_SIZE, K.stream_of(self.appended))
+        K.check(rc, "KiviStreamBatch.plan")
+        return act   # keeps a converted mask alive until the launch is queued
+
+    def _append(self, k_new, v_new):
+        B, KVH, D = self.shape
+        win = (K._vp * 6)(*[K.ptr(self.t[n]) if self.t[n].numel() else None for n in _WIN_KEYS])
+        rc = K.lib.kvdec_kivi_stream_append_seqs(K.ptr(k_new), K.ptr(v_new), K.ptr(self.t["k_ring"]),
+                                                 K.ptr(self.t["v_ring"]), win, B, KVH, D, self.cap,
+                                                 self.n_groups, K.ptr(self.plan), GROUP_SIZE, QUANT_BITS,
+                                                 K.stream_of(self.t["k_ring"]))
+        K.check(rc, "KiviStreamBatch.append")
+
+    def append(self, k_new, v_new, active=None):
+        """Append one token to every active sequence: k_new, v_new [B, KVH, D]
+        fp16 (rows of inactive sequences are ignored); active: [B] bool or
+        int tensor on the GPU, None = all."""
+        B, KVH, D = self.shape
+        k_new = k_new.reshape(B, KVH, D).contiguous()
+        v_new = v_new.reshape(B, KVH, D).contiguous()
+        _checks.require_gpu_tensor("k_new", k_new, ndim=3)
+        _checks.require_gpu_tensor("v_new", v_new, ndim=3)
+        _checks.require_same_device(("k_new", k_new), ("v_new", v_new), ("k_ring", self.t["k_ring"]))
+        act = self._plan(active)
+        self._append(k_new, v_new)
+        del act
+
+    def reserve(self, active=None):
+        """Advance every active sequence by one token and return the ring row
+        each one takes ([B] int32 on the GPU, -1 for inactive sequences): the
+        producer of K and V writes them to k_ring[b, :, row[b]] and
+        v_ring[b, :, row[b]].  Evictions due at this token are enqueued here."""
+        act = self._plan(active)
+        self._append(None, None)
+        del act
+        return self.plan[:, 0]
+
+    def attend(self, q, sm_scale=None):
+        """Decode attention of q [B, H, D] fp16 over each sequence's cache."""
+        B, KVH, D = self.shape
+        _checks.require_gpu_tensor("q", q, ndim=3)
+        _checks.require_shape("q", q, (B, q.shape[1], D))
+        _checks.require_same_device(("q", q), ("k_ring", self.t["k_ring"]))
+        o = torch.empty_like(q)
+        if sm_scale is None:
+            sm_scale = D_HEAD**-0.5
+        names = _SINK_KEYS + _WIN_KEYS
+        arr = (K._vp * 12)(*[K.ptr(self.t[n]) if self.t[n].numel() else None for n in names])
+        rc = K.lib.kvdec_kivi_stream_decode_seqs(K.ptr(q), K.ptr(self.t["k_ring"]), K.ptr(self.t["v_ring"]),
+                                                 arr, K.ptr(o), K.ptr(self.ring), B, q.shape[1], KVH,
+                                                 self.sink, self.n_groups, self.cap, GROUP_SIZE, QUANT_BITS,
+                                                 float(sm_scale), K.stream_of(q))
+        K.check(rc, "KiviStreamBatch.attend")
+        return o

@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 17
+    assert len(funcs) == 20
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -294,6 +294,29 @@ def test_sparse_varlen_validation():
     assert _svarlen(layout=5) == E["UNSUPPORTED"]
     assert _svarlen(layout=K.LAYOUT_RING, W=0) == E["WINDOW"]
     assert _svarlen() == E["WORKSPACE"]
+
+
+def test_stream_seqs_validation():
+    L = K.lib
+    assert L.kvdec_kivi_stream_plan(None, None, FAKE, FAKE, 4, 128, 160, 4, 32, None) == E["NULL"]
+    assert L.kvdec_kivi_stream_plan(FAKE, None, FAKE, FAKE, 4, 128, 160, 4, 64, None) == E["UNSUPPORTED"]
+    assert L.kvdec_kivi_stream_plan(FAKE, None, FAKE, FAKE, 0, 128, 160, 4, 32, None) == E["SHAPE"]
+    assert L.kvdec_kivi_stream_plan(FAKE, None, FAKE, FAKE, 4, 128, 192, 4, 32, None) == E["WINDOW"]
+    assert L.kvdec_kivi_stream_plan(FAKE, None, FAKE, FAKE, 4, 100, 132, 4, 32, None) == E["WINDOW"]
+    win = (K._vp * 6)(*([0x1000] * 6))
+    ap = L.kvdec_kivi_stream_append_seqs
+    assert ap(FAKE, None, FAKE, FAKE, win, 4, 8, 128, 160, 4, FAKE, 32, 2, None) == E["NULL"]
+    assert ap(None, None, FAKE, FAKE, win, 4, 8, 128, 160, 4, None, 32, 2, None) == E["NULL"]
+    assert ap(None, None, FAKE, FAKE, win, 4, 8, 128, 160, 4, FAKE, 32, 4, None) == E["BITS"]
+    assert ap(None, None, FAKE, FAKE, win, 4, 8, 100, 160, 4, FAKE, 32, 2, None) == E["DGROUP"]
+    assert ap(None, None, FAKE, FAKE, win, 4, 8, 128, 170, 4, FAKE, 32, 2, None) == E["WINDOW"]
+    assert ap(None, None, FAKE, FAKE, None, 4, 8, 128, 160, 4, FAKE, 32, 2, None) == E["NULL"]
+    arr = (K._vp * 12)(*([0x1000] * 12))
+    dec = L.kvdec_kivi_stream_decode_seqs
+    assert dec(FAKE, FAKE, FAKE, arr, FAKE, None, 4, 64, 8, 4, 4, 160, 32, 2, 0.088, None) == E["NULL"]
+    assert dec(FAKE, FAKE, FAKE, arr, FAKE, FAKE, 4, 64, 8, 0, 4, 160, 32, 2, 0.088, None) == E["WINDOW"]
+    assert dec(FAKE, FAKE, FAKE, arr, FAKE, FAKE, 4, 64, 8, 4, 4, 48, 32, 2, 0.088, None) == E["WINDOW"]
+    assert dec(FAKE, FAKE, FAKE, arr, FAKE, FAKE, 4, 60, 8, 4, 4, 160, 32, 2, 0.088, None) == E["SHAPE"]
 
 
 def _build(**kw):
