@@ -31,3 +31,33 @@ def test_ring_bookkeeping_matches_token_model():
             assert st.count == len(rows)
             assert [(st.start + i) % st.cap for i in range(st.count)] == rows
             assert not n_groups or [(st.next_slot + i) % n_groups for i in range(n_groups)] == slots
+
+
+def _state_from_count(n, R, G, cap, n_groups):
+    """The closed form kvdec_kivi_stream_plan uses: the ring state after n
+    appends, and the step taken by append n + 1."""
+    e = n // G
+    start, count = (G * e) % cap, R + n % G
+    row = (start + count) % cap
+    if count + 1 == cap:
+        step = (row, start // G, e % n_groups if n_groups else -1)
+        after = ((start + G) % cap, R)
+    else:
+        step = (row, -1, -1)
+        after = (start, count + 1)
+    return (start, count), step, after
+
+
+def test_plan_closed_form_matches_ring_state():
+    """The per-sequence plan kernel derives each step from the append count
+    alone; that closed form must agree with RingState.append() step by step."""
+    R, G = 128, 32
+    for n_groups in (0, 1, 4, 28):
+        cap = R + G
+        st = RingState(cap=cap, residual=R, n_groups=n_groups, count=R)
+        for n in range(9 * G + 5):
+            before, step, after = _state_from_count(n, R, G, cap, n_groups)
+            assert before == (st.start, st.count), n
+            row, blk, slot = st.append()
+            assert step == (row, blk, slot if blk >= 0 else -1), n
+            assert after == (st.start, st.count), n
