@@ -247,32 +247,26 @@ int kvdec_kivi_stream_decode(const void* q, const void* k_ring,
 
 /*
  * The same cache with one ring state per sequence, for sequences that join
- * (a new prefill in their batch slot) and pause independently.  All three
- * entry points are asynchronous on `stream`; nothing is read back.
+ * (a new prefill in their batch slot) and pause independently.  Both entry
+ * points are asynchronous on `stream`; nothing is read back.
  *
- * kvdec_kivi_stream_plan: one step of the bookkeeping.  appended [B] int32
- * counts the tokens appended to each sequence since its prefill (set it to
- * 0 when a prefill is written into the slot); active [B] int32 (NULL: all)
- * selects the sequences that take a token this step.  Writes plan [B][3] =
- * {row, evict_block, evict_slot} (-1 = none) for the append and ring [B][2]
- * = {start, count} after it for the decode, and advances `appended`.
+ * kvdec_kivi_stream_step: one token step.  appended [B] int32 counts the
+ * tokens appended to each sequence since its prefill (set it to 0 when a
+ * prefill is written into the slot); active [B] int32 (NULL: all) selects
+ * the sequences that take a token.  Each active sequence's next ring row
+ * gets k_new / v_new [B, KVH, D] (both NULL: the producer writes the rows
+ * itself, after this call), and a ring that fills has its oldest 32-row
+ * block quantized into its oldest window-old slot.  Writes plan [B][3] =
+ * {row, evict block, evict slot} taken (-1 = none), ring [B][2] = {start,
+ * count} after the step, and advances `appended`.  arrive [B] int32 is
+ * scratch the caller zeroes once (the kernel leaves it zero).
  * ring_cap == residual + group.
  */
-int kvdec_kivi_stream_plan(int32_t* appended, const int32_t* active, int32_t* plan,
-                           int32_t* ring, int64_t B, int32_t residual, int32_t ring_cap,
-                           int32_t n_groups, int32_t group, void* stream);
-
-/*
- * kvdec_kivi_stream_append_seqs: kvdec_kivi_stream_append with the row and
- * the eviction of each sequence taken from plan [B][3] (entries outside the
- * ring are ignored).  k_new / v_new both NULL: only the evictions (the
- * producer writes the rows itself).
- */
-int kvdec_kivi_stream_append_seqs(const void* k_new, const void* v_new, void* k_ring,
-                                  void* v_ring, void* const* win, int64_t B, int32_t KVH,
-                                  int32_t D, int32_t ring_cap, int32_t n_groups,
-                                  const int32_t* plan, int32_t group, int32_t bits,
-                                  void* stream);
+int kvdec_kivi_stream_step(const void* k_new, const void* v_new, void* k_ring, void* v_ring,
+                           void* const* win, int32_t* appended, const int32_t* active,
+                           int32_t* arrive, int32_t* plan, int32_t* ring, int64_t B,
+                           int32_t KVH, int32_t D, int32_t residual, int32_t ring_cap,
+                           int32_t n_groups, int32_t group, int32_t bits, void* stream);
 
 /*
  * kvdec_kivi_stream_decode_seqs: kvdec_kivi_stream_decode with each

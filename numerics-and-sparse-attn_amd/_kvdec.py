@@ -61,9 +61,8 @@ SIGNATURES = {
     "kvdec_kivi_stream_decode": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _i64, _i32,
                                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                                 _vp]),
-    "kvdec_kivi_stream_plan": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
-    "kvdec_kivi_stream_append_seqs": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.POINTER(_vp), _i64, _i32,
-                                                     _i32, _i32, _i32, _vp, _i32, _i32, _vp]),
+    "kvdec_kivi_stream_step": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _vp, _vp, _vp,
+                                              _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "kvdec_kivi_stream_decode_seqs": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _vp, _i64,
                                                      _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                                      _vp]),

@@ -464,32 +464,48 @@ struct StreamArgs {
   uint8_t* vp;             // [pairs][nwg * group][D / 4]
   _Float16* vs;            // [pairs][nwg * group][D / group]
   _Float16* vz;
-  const int32_t* plan;     // per sequence {row, evict block, evict slot} [B][3], or null
-  int D, cap, row, blk, slot, nwg, KVH;
+  // per-sequence bookkeeping (all null for one shared ring state)
+  int32_t* appended;       // [B] tokens appended since each sequence's prefill
+  const int32_t* active;   // [B] or null (all)
+  int32_t* arrive;         // [B] workgroups done this step (0 between launches)
+  int32_t* plan;           // [B][3] {row, evict block, evict slot} taken this step
+  int32_t* ring;           // [B][2] {start, count} after this step
+  int D, cap, row, blk, slot, nwg, KVH, residual;
 };
 
-__global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
-  const int64_t pair = blockIdx.x;
-  const int D = a.D;
-  int row = a.row, blk = a.blk, slot = a.slot;
-  if (a.plan) {
-    // this sequence's step; entries outside the ring mean "no write" /
-    // "no eviction" (the plan is device data the host did not check)
-    const int32_t* pb = a.plan + 3 * (pair / a.KVH);
-    row = pb[0];
-    blk = pb[1];
-    slot = pb[2];
-    if (row < 0 || row >= a.cap) row = -1;
-    if (blk < 0 || blk >= a.cap / kGroup || a.nwg <= 0 || slot < 0 || slot >= a.nwg ||
-        (row >= 0 && row / kGroup == blk))
-      blk = -1;
-  }
-  if (a.k_new && row >= 0)
-    for (int i = threadIdx.x; i < D; i += blockDim.x) {
-      a.k_ring[((size_t)pair * a.cap + row) * D + i] = a.k_new[(size_t)pair * D + i];
-      a.v_ring[((size_t)pair * a.cap + row) * D + i] = a.v_new[(size_t)pair * D + i];
+// Ring bookkeeping of one sequence of a decode-time KIVI cache.  The state
+// after n appended tokens is fixed by n: n / 32 evictions, so the residual
+// ring holds rows [start, start + count) mod cap with start = 32 (n / 32)
+// mod cap and count = residual + n mod 32, and the oldest window-old group
+// sits in slot (n / 32) mod n_groups.  An active step takes row (start +
+// count) mod cap; when that fills the ring, its oldest 32-row block is
+// quantized into the oldest group's slot.  Returns the step ({row, block,
+// slot}, -1 = none) and the state after it.
+struct RingStep {
+  int row, blk, slot, start, count;
+};
+
+__device__ __forceinline__ RingStep ring_step(int n, bool act, int residual, int cap, int ngroups) {
+  const int e = n / kGroup;
+  RingStep r{-1, -1, -1, (int)(((int64_t)kGroup * e) % cap), residual + n % kGroup};
+  if (act) {
+    r.row = (r.start + r.count) % cap;
+    if (r.count + 1 == cap) {
+      r.blk = r.start / kGroup;
+      r.slot = ngroups > 0 ? e % ngroups : -1;
+      r.start = (r.start + kGroup) % cap;
+      r.count = residual;
+    } else {
+      r.count += 1;
     }
-  if (blk < 0) return;
+  }
+  return r;
+}
+
+// Quantize ring rows [32 blk, +32) of one (b, kv) head into window-old slot
+// `slot` (K per channel, V per token, the quantizers' exact formulas).
+__device__ __forceinline__ void evict_block(const StreamArgs& a, int64_t pair, int blk, int slot) {
+  const int D = a.D;
   const size_t blk0 = (size_t)pair * a.cap + (size_t)blk * kGroup;   // first ring row of the block
   const size_t g = (size_t)pair * a.nwg + slot;
   // K: one thread per channel, its 32 tokens (per-channel group)
@@ -521,43 +537,46 @@ __global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
   }
 }
 
-// Per-sequence ring bookkeeping of a decode-time KIVI cache, one thread per
-// sequence.  appended[b] counts the tokens appended since sequence b's
-// prefill; the state after n appends is fixed by n: n / 32 evictions, so the
-// residual ring holds rows [start, start + count) mod cap with
-// start = 32 (n / 32) mod cap and count = residual + n mod 32, and the
-// oldest window-old group sits in slot (n / 32) mod n_groups.  An active
-// sequence takes row (start + count) mod cap; when that fills the ring its
-// oldest 32-row block is quantized into the oldest group's slot.  Writes
-// plan[b] = {row, evict block, evict slot} (-1: none) and ring[b] =
-// {start, count} after the step, and advances appended[b].
-__global__ __launch_bounds__(256) void stream_plan_kernel(int32_t* appended, const int32_t* active,
-                                                          int32_t* plan, int32_t* ring, int64_t B,
-                                                          int residual, int cap, int ngroups) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= B) return;
-  const int n = max(appended[b], 0);
-  const int e = n / kGroup;
-  int start = (int)(((int64_t)kGroup * e) % cap);
-  int count = residual + n % kGroup;
-  int32_t p0 = -1, p1 = -1, p2 = -1;
-  if (!active || active[b]) {
-    p0 = (start + count) % cap;
-    if (count + 1 == cap) {            // the ring is full: evict its oldest block
-      p1 = start / kGroup;
-      p2 = ngroups > 0 ? e % ngroups : -1;
-      start = (start + kGroup) % cap;
-      count = residual;
-    } else {
-      count += 1;
-    }
-    appended[b] = n + 1;
+__global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
+  const int64_t pair = blockIdx.x;
+  const int D = a.D;
+  int row = a.row, blk = a.blk, slot = a.slot;
+  const int64_t b = a.appended ? pair / a.KVH : 0;
+  RingStep rs{};
+  int n = 0;
+  bool act = false;
+  if (a.appended) {
+    // this sequence's step, from its append count (read by every workgroup
+    // of the sequence before any of them advances it, below)
+    n = max(a.appended[b], 0);
+    act = !a.active || a.active[b] != 0;
+    rs = ring_step(n, act, a.residual, a.cap, a.nwg);
+    row = rs.row;
+    blk = a.nwg > 0 ? rs.blk : -1;
+    slot = rs.slot;
   }
-  plan[3 * b] = p0;
-  plan[3 * b + 1] = p1;
-  plan[3 * b + 2] = p2;
-  ring[2 * b] = start;
-  ring[2 * b + 1] = count;
+  if (a.k_new && row >= 0)
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+      a.k_ring[((size_t)pair * a.cap + row) * D + i] = a.k_new[(size_t)pair * D + i];
+      a.v_ring[((size_t)pair * a.cap + row) * D + i] = a.v_new[(size_t)pair * D + i];
+    }
+  if (blk >= 0) evict_block(a, pair, blk, slot);
+  if (a.appended) {
+    // the last of the sequence's KVH workgroups to arrive records the step
+    // and advances the count.  Every workgroup's threads have consumed their
+    // load of the count before its barrier, so no fence is needed; the
+    // writes reach the next launch at the kernel boundary.
+    __syncthreads();
+    if (threadIdx.x == 0 && atomicAdd(a.arrive + b, 1) == a.KVH - 1) {
+      a.arrive[b] = 0;
+      a.appended[b] = n + (act ? 1 : 0);
+      a.plan[3 * b] = rs.row;
+      a.plan[3 * b + 1] = rs.blk;
+      a.plan[3 * b + 2] = rs.blk >= 0 ? rs.slot : -1;
+      a.ring[2 * b] = rs.start;
+      a.ring[2 * b + 1] = rs.count;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -757,6 +776,7 @@ int kvdec_kivi_stream_append(const void* k_new, const void* v_new, void* k_ring,
   a.v_ring = static_cast<_Float16*>(v_ring);
   a.D = D;
   a.cap = ring_cap;
+  a.KVH = KVH;
   a.row = row;
   // a window == residual cache has no window-old groups: the block is dropped
   a.blk = (evict_block >= 0 && n_groups > 0) ? evict_block : -1;
@@ -776,31 +796,20 @@ int kvdec_kivi_stream_append(const void* k_new, const void* v_new, void* k_ring,
   return launch_status();
 }
 
-int kvdec_kivi_stream_plan(int32_t* appended, const int32_t* active, int32_t* plan,
-                           int32_t* ring, int64_t B, int32_t residual, int32_t ring_cap,
-                           int32_t n_groups, int32_t group, void* stream) {
-  if (!appended || !plan || !ring) return KVDEC_E_NULL;
-  if (group != kGroup) return KVDEC_E_UNSUPPORTED;
-  if (B < 1 || n_groups < 0) return KVDEC_E_SHAPE;
-  if (residual < kGroup || residual % kGroup != 0 || ring_cap != residual + kGroup)
-    return KVDEC_E_WINDOW;
-  hipLaunchKernelGGL(stream_plan_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), appended, active, plan, ring, B, residual,
-                     ring_cap, n_groups);
-  return launch_status();
-}
-
-int kvdec_kivi_stream_append_seqs(const void* k_new, const void* v_new, void* k_ring, void* v_ring,
-                                  void* const* win, int64_t B, int32_t KVH, int32_t D,
-                                  int32_t ring_cap, int32_t n_groups, const int32_t* plan,
-                                  int32_t group, int32_t bits, void* stream) {
-  if (!k_ring || !v_ring || !plan || (!k_new) != (!v_new)) return KVDEC_E_NULL;
+int kvdec_kivi_stream_step(const void* k_new, const void* v_new, void* k_ring, void* v_ring,
+                           void* const* win, int32_t* appended, const int32_t* active,
+                           int32_t* arrive, int32_t* plan, int32_t* ring, int64_t B, int32_t KVH,
+                           int32_t D, int32_t residual, int32_t ring_cap, int32_t n_groups,
+                           int32_t group, int32_t bits, void* stream) {
+  if (!k_ring || !v_ring || !appended || !arrive || !plan || !ring || (!k_new) != (!v_new))
+    return KVDEC_E_NULL;
   if (bits != 2) return KVDEC_E_BITS;
   if (group != kGroup) return KVDEC_E_UNSUPPORTED;
-  if (B < 1 || KVH < 1 || D < 1 || B * (int64_t)KVH > 0x7fffffffLL) return KVDEC_E_SHAPE;
+  if (B < 1 || KVH < 1 || D < 1 || B * (int64_t)KVH > 0x7fffffffLL || n_groups < 0)
+    return KVDEC_E_SHAPE;
   if (D % kGroup != 0) return KVDEC_E_DGROUP;
-  if (ring_cap < 2 * kGroup || ring_cap % kGroup != 0) return KVDEC_E_WINDOW;
-  if (n_groups < 0) return KVDEC_E_SHAPE;
+  if (residual < kGroup || residual % kGroup != 0 || ring_cap != residual + kGroup)
+    return KVDEC_E_WINDOW;
   if (n_groups > 0) {
     if (!win) return KVDEC_E_NULL;
     for (int i = 0; i < 6; ++i)
@@ -811,11 +820,16 @@ int kvdec_kivi_stream_append_seqs(const void* k_new, const void* v_new, void* k_
   a.v_new = static_cast<const _Float16*>(v_new);
   a.k_ring = static_cast<_Float16*>(k_ring);
   a.v_ring = static_cast<_Float16*>(v_ring);
+  a.appended = appended;
+  a.active = active;
+  a.arrive = arrive;
   a.plan = plan;
+  a.ring = ring;
   a.D = D;
   a.cap = ring_cap;
   a.nwg = n_groups;
   a.KVH = KVH;
+  a.residual = residual;
   if (n_groups > 0) {
     a.kp = static_cast<uint8_t*>(win[0]);
     a.ks = static_cast<_Float16*>(win[1]);

@@ -203,10 +203,10 @@ class KiviStreamBatch:
     """Decode-time KIVI cache whose B sequences keep separate ring states,
     for continuous batching: a sequence can take a new prefill in its batch
     slot (admit) and sit out steps (the `active` mask), while the others go
-    on.  The bookkeeping lives on the GPU (kvdec_kivi_stream_plan: a token
-    count per sequence, from which each step's ring row, eviction and ring
-    state follow), so a step is three launches and no host round trip:
-    plan, append (quantize-on-evict), attend.  Each sequence's state equals
+    on.  The bookkeeping lives on the GPU (a token count per sequence, from
+    which each step's ring row, eviction and ring state follow, kept by the
+    append kernel itself), so a step is two launches and no host round
+    trip: the step (append, quantize-on-evict, bookkeeping) and attend.  Each sequence's state equals
     a KiviStreamCache of that sequence alone after the same appends."""
 
     def __init__(self, tensors, window, sink, residual):
@@ -217,6 +217,7 @@ class KiviStreamBatch:
         B = tensors["k_ring"].shape[0]
         dev = tensors["k_ring"].device
         self.appended = torch.zeros(B, dtype=torch.int32, device=dev)   # tokens since each prefill
+        self.arrive = torch.zeros(B, dtype=torch.int32, device=dev)     # kernel scratch, stays zero
         self.plan = torch.full((B, 3), -1, dtype=torch.int32, device=dev)
         self.ring = torch.tensor([[0, self.residual]] * B, dtype=torch.int32, device=dev)
 
@@ -245,27 +246,20 @@ class KiviStreamBatch:
         self.ring[b, 0] = 0
         self.ring[b, 1] = self.residual
 
-    def _plan(self, active):
+    def _step(self, k_new, v_new, active):
         B, KVH, D = self.shape
         act = None
         if active is not None:
             act = active.to(device=self.appended.device, dtype=torch.int32).contiguous()
             _checks.require_gpu_tensor("active", act, dtypes=(torch.int32,), ndim=1)
             _checks.require_shape("active", act, (B,))
-        rc = K.lib.kvdec_kivi_stream_plan(K.ptr(self.appended), K.ptr(act) if act is not None else None,
-                                          K.ptr(self.plan), K.ptr(self.ring), B, self.residual, self.cap,
-                                          self.n_groups, GROUP_SIZE, K.stream_of(self.appended))
-        K.check(rc, "KiviStreamBatch.plan")
-        return act   # keeps a converted mask alive until the launch is queued
-
-    def _append(self, k_new, v_new):
-        B, KVH, D = self.shape
         win = (K._vp * 6)(*[K.ptr(self.t[n]) if self.t[n].numel() else None for n in _WIN_KEYS])
-        rc = K.lib.kvdec_kivi_stream_append_seqs(K.ptr(k_new), K.ptr(v_new), K.ptr(self.t["k_ring"]),
-                                                 K.ptr(self.t["v_ring"]), win, B, KVH, D, self.cap,
-                                                 self.n_groups, K.ptr(self.plan), GROUP_SIZE, QUANT_BITS,
-                                                 K.stream_of(self.t["k_ring"]))
-        K.check(rc, "KiviStreamBatch.append")
+        rc = K.lib.kvdec_kivi_stream_step(K.ptr(k_new), K.ptr(v_new), K.ptr(self.t["k_ring"]),
+                                          K.ptr(self.t["v_ring"]), win, K.ptr(self.appended), K.ptr(act),
+                                          K.ptr(self.arrive), K.ptr(self.plan), K.ptr(self.ring), B, KVH, D,
+                                          self.residual, self.cap, self.n_groups, GROUP_SIZE, QUANT_BITS,
+                                          K.stream_of(self.t["k_ring"]))
+        K.check(rc, "KiviStreamBatch.step")
 
     def append(self, k_new, v_new, active=None):
         """Append one token to every active sequence: k_new, v_new [B, KVH, D]
@@ -277,18 +271,14 @@ class KiviStreamBatch:
         _checks.require_gpu_tensor("k_new", k_new, ndim=3)
         _checks.require_gpu_tensor("v_new", v_new, ndim=3)
         _checks.require_same_device(("k_new", k_new), ("v_new", v_new), ("k_ring", self.t["k_ring"]))
-        act = self._plan(active)
-        self._append(k_new, v_new)
-        del act
+        self._step(k_new, v_new, active)
 
     def reserve(self, active=None):
         """Advance every active sequence by one token and return the ring row
         each one takes ([B] int32 on the GPU, -1 for inactive sequences): the
         producer of K and V writes them to k_ring[b, :, row[b]] and
         v_ring[b, :, row[b]].  Evictions due at this token are enqueued here."""
-        act = self._plan(active)
-        self._append(None, None)
-        del act
+        self._step(None, None, active)
         return self.plan[:, 0]
 
     def attend(self, q, sm_scale=None):

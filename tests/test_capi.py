@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 20
+    assert len(funcs) == 19
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -298,19 +298,27 @@ def test_sparse_varlen_validation():
 
 def test_stream_seqs_validation():
     L = K.lib
-    assert L.kvdec_kivi_stream_plan(None, None, FAKE, FAKE, 4, 128, 160, 4, 32, None) == E["NULL"]
-    assert L.kvdec_kivi_stream_plan(FAKE, None, FAKE, FAKE, 4, 128, 160, 4, 64, None) == E["UNSUPPORTED"]
-    assert L.kvdec_kivi_stream_plan(FAKE, None, FAKE, FAKE, 0, 128, 160, 4, 32, None) == E["SHAPE"]
-    assert L.kvdec_kivi_stream_plan(FAKE, None, FAKE, FAKE, 4, 128, 192, 4, 32, None) == E["WINDOW"]
-    assert L.kvdec_kivi_stream_plan(FAKE, None, FAKE, FAKE, 4, 100, 132, 4, 32, None) == E["WINDOW"]
     win = (K._vp * 6)(*([0x1000] * 6))
-    ap = L.kvdec_kivi_stream_append_seqs
-    assert ap(FAKE, None, FAKE, FAKE, win, 4, 8, 128, 160, 4, FAKE, 32, 2, None) == E["NULL"]
-    assert ap(None, None, FAKE, FAKE, win, 4, 8, 128, 160, 4, None, 32, 2, None) == E["NULL"]
-    assert ap(None, None, FAKE, FAKE, win, 4, 8, 128, 160, 4, FAKE, 32, 4, None) == E["BITS"]
-    assert ap(None, None, FAKE, FAKE, win, 4, 8, 100, 160, 4, FAKE, 32, 2, None) == E["DGROUP"]
-    assert ap(None, None, FAKE, FAKE, win, 4, 8, 128, 170, 4, FAKE, 32, 2, None) == E["WINDOW"]
-    assert ap(None, None, FAKE, FAKE, None, 4, 8, 128, 160, 4, FAKE, 32, 2, None) == E["NULL"]
+
+    def step(**kw):
+        a = dict(kn=None, vn=None, kr=FAKE, vr=FAKE, win=win, app=FAKE, act=None, arr=FAKE, plan=FAKE,
+                 ring=FAKE, B=4, KVH=8, D=128, R=128, cap=160, ng=4, group=32, bits=2)
+        a.update(kw)
+        return L.kvdec_kivi_stream_step(a["kn"], a["vn"], a["kr"], a["vr"], a["win"], a["app"], a["act"],
+                                        a["arr"], a["plan"], a["ring"], a["B"], a["KVH"], a["D"], a["R"],
+                                        a["cap"], a["ng"], a["group"], a["bits"], None)
+
+    assert step(app=None) == E["NULL"]
+    assert step(arr=None) == E["NULL"]
+    assert step(kn=FAKE) == E["NULL"]                  # one of the pair missing
+    assert step(win=None) == E["NULL"]
+    assert step(bits=4) == E["BITS"]
+    assert step(group=64) == E["UNSUPPORTED"]
+    assert step(B=0) == E["SHAPE"]
+    assert step(ng=-1) == E["SHAPE"]
+    assert step(D=100) == E["DGROUP"]
+    assert step(cap=192) == E["WINDOW"]
+    assert step(R=100, cap=132) == E["WINDOW"]
     arr = (K._vp * 12)(*([0x1000] * 12))
     dec = L.kvdec_kivi_stream_decode_seqs
     assert dec(FAKE, FAKE, FAKE, arr, FAKE, None, 4, 64, 8, 4, 4, 160, 32, 2, 0.088, None) == E["NULL"]

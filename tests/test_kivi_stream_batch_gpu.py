@@ -18,10 +18,11 @@ S, R, G = 4, 128, 32
 
 
 def test_plan_matches_host_ring_state(device):
-    """kvdec_kivi_stream_plan over 150 steps with random active masks: plan
-    and ring state equal RingState.append() per sequence."""
+    """The on-GPU bookkeeping of kvdec_kivi_stream_step over 150 steps with
+    random active masks: the step taken and the ring state after it equal
+    RingState.append() per sequence."""
     from kivi_stream import KiviStreamBatch, RingState
-    B, KVH, D, W = 6, 1, 128, 256
+    B, KVH, D, W = 6, 3, 128, 256
     k = torch.zeros(B, KVH, S + W, D, dtype=torch.float16, device=device)
     cache = KiviStreamBatch.from_prefill(k, k, W)
     host_rings = [RingState(cap=R + G, residual=R, n_groups=(W - R) // G, count=R) for _ in range(B)]
@@ -29,7 +30,7 @@ def test_plan_matches_host_ring_state(device):
     say("stream plan vs host")
     for step in range(150):
         active = rng.random(B) < 0.7
-        cache._plan(torch.from_numpy(active).to(device))
+        cache._step(None, None, torch.from_numpy(active).to(device))
         plan, ring = host(cache.plan), host(cache.ring)
         for b in range(B):
             if active[b]:
