@@ -34,7 +34,7 @@ def test_ring_bookkeeping_matches_token_model():
 
 
 def _state_from_count(n, R, G, cap, n_groups):
-    """The closed form kvdec_kivi_stream_plan uses: the ring state after n
+    """The closed form kvdec_kivi_stream_step uses: the ring state after n
     appends, and the step taken by append n + 1."""
     e = n // G
     start, count = (G * e) % cap, R + n % G
@@ -49,7 +49,7 @@ def _state_from_count(n, R, G, cap, n_groups):
 
 
 def test_plan_closed_form_matches_ring_state():
-    """The per-sequence plan kernel derives each step from the append count
+    """The per-sequence step kernel derives each step from the append count
     alone; that closed form must agree with RingState.append() step by step."""
     R, G = 128, 32
     for n_groups in (0, 1, 4, 28):
