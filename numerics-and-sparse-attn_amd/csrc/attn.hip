@@ -16,7 +16,9 @@
 // KIVI units have two queues: the fp16 residual tiles go to the first waves
 // (one each while there are enough waves), the quantized tiles (window-old
 // groups, then the sink group) to the others; a wave that finishes its
-// residual tiles joins the quantized queue.
+// residual tiles joins the quantized queue.  When a few quantized tiles are
+// left over for the residual waves, the waves that take them hand their
+// fp16 tiles to other residual waves, balancing the SIMDs' VALU load.
 
 #include "kvdec_device.h"
 #include "kvdec.h"
@@ -574,6 +576,13 @@ struct KiviSrcBase {
     const int nqw = kWaves - nrw;
     const bool dyn_q = qit.n > n_static_q();
     const bool dyn = dyn_q || (nqw == 0 && n_res() > 2 * nrw);   // any dynamic queue
+    // Waves w and w + 4 share a SIMD, whose VALU the quantized steps
+    // saturate.  When only e <= nrw / 2 residual waves get an extra
+    // quantized tile (static queue), residual wave rw < e steps that tile
+    // alone and residual wave e + rw takes its fp16 tile: no SIMD then
+    // carries a quantized and an fp16 step more than the others.
+    const int extra = nqw > 0 && !dyn_q ? max(qit.n - nqw, 0) : 0;
+    const bool hand = extra > 0 && 2 * extra <= nrw;
 #if KVDEC_RES_FIRST
     const int rw = wave, qw = wave - nrw;
 #else
@@ -592,7 +601,24 @@ struct KiviSrcBase {
       rit.rot = 0;
       rit.R = R;
       bool has_q = false;
-      if (nqw > 0) {
+      if (hand && rw < extra) {
+        Ring<QItems<false>> qring;
+        ring_begin(qonly, qring, nqw + rw, qonly.n, lane);
+        sync(c, true);
+        if constexpr (MODE != kOneRange) c.R = R;
+        ring_run_static(qonly, qring, qref, c);
+        publish_ml(P, st, c.lds, lane, wave);
+        publish_q<false>(qs, c.slot, lane);
+        return;
+      }
+      if (hand) {
+        // loads issued after the barrier, behind every quantized tile's
+        sync(c, true);
+        if constexpr (MODE != kOneRange) c.R = R;
+        Ring<F16Items> rring;
+        ring_begin(rit, rring, rw, rw - extra < extra ? rw - extra : rit.n, lane);
+        ring_run_static(rit, rring, st, c);
+      } else if (nqw > 0) {
         // one extra quantized tile (if there is one) and one residual tile.
         // The residual tile's loads are issued after the workgroup barrier,
         // behind the loads of every quantized tile: a CU serves its loads
