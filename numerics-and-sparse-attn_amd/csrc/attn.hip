@@ -193,8 +193,7 @@ __device__ __forceinline__ uint32_t row_off(int head, int chunk) {
 
 __device__ __forceinline__ void publish_ml(const AttnCommon& P, WaveState& st, char* lds, int lane,
                                            int wave) {
-  st.l += __shfl_xor(st.l, 16);
-  st.l += __shfl_xor(st.l, 32);
+  st.l = group_sum(st.l);
   const int n = lane & 15, g = lane >> 4;
   if (n < P.G && g == 0) {
     reinterpret_cast<float*>(lds + kLdsM)[wave * kMaxGroup + n] = st.m;
@@ -682,6 +681,18 @@ struct KiviRingSrc : KiviSrcBase<kSeqRings> {};
 template <class Src>
 __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) {
   extern __shared__ __align__(16) char lds[];
+  // Bring every 64-byte line of the kernel arguments into the scalar cache
+  // in one round trip: the compiler fetches the fields where they are first
+  // used, which would otherwise cost a cache miss per line in series.
+  {
+    constexpr int kArgLines = (int)(sizeof(AttnCommon) + sizeof(Src) + 63) / 64;
+    static_assert(kArgLines <= 5, "kernel arguments span more lines than are touched");
+    const cint32* ka = (const cint32*)__builtin_amdgcn_kernarg_segment_ptr();
+    int32_t x[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
+    asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]));
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int split = (int)(blockIdx.x % (unsigned)P.n_splits);

@@ -74,6 +74,29 @@ __device__ __forceinline__ uint32_t pk_sub_f16(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) - __builtin_bit_cast(half2v, b));
 }
 
+// Sum / max over the four lanes t, t + 16, t + 32, t + 48 (the lane groups g
+// of one MFMA row), left in all four.  Each step swaps rows between two
+// copies of x with a VALU lane swap (no LDS round trip): after
+// v_permlane16_swap the copies hold rows (0, 0, 2, 2) and (1, 1, 3, 3), after
+// v_permlane32_swap the halves (lo, lo) and (hi, hi), so combining the two
+// copies combines lanes L and L ^ 16, then L and L ^ 32.
+__device__ __forceinline__ float group_sum(float x) {
+  const uint32_t a = __builtin_bit_cast(uint32_t, x);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+  const float y = __builtin_bit_cast(float, (uint32_t)s16[0]) + __builtin_bit_cast(float, (uint32_t)s16[1]);
+  const uint32_t b = __builtin_bit_cast(uint32_t, y);
+  const auto s32 = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return __builtin_bit_cast(float, (uint32_t)s32[0]) + __builtin_bit_cast(float, (uint32_t)s32[1]);
+}
+__device__ __forceinline__ float group_max(float x) {
+  const uint32_t a = __builtin_bit_cast(uint32_t, x);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+  const float y = fmaxf(__builtin_bit_cast(float, (uint32_t)s16[0]), __builtin_bit_cast(float, (uint32_t)s16[1]));
+  const uint32_t b = __builtin_bit_cast(uint32_t, y);
+  const auto s32 = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)s32[0]), __builtin_bit_cast(float, (uint32_t)s32[1]));
+}
+
 __device__ __forceinline__ float4v mfma16x16x32(u32x4 a, half8 b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(a), b, c, 0, 0, 0);
 }
@@ -180,16 +203,19 @@ __device__ __forceinline__ void tile_body(KOp&& kop, VOp&& vop, uint32_t valid,
   for (int j = 1; j < 8; ++j) lmax = fmaxf(lmax, x[j]);
 
   // Refresh the reference max only if some lane's tile max exceeds it by
-  // more than kRescaleSlack (wave-uniform branch).
+  // more than kRescaleSlack (wave-uniform branch).  While every head is at
+  // the sentinel nothing has been accumulated (l and O are zero), so the
+  // wave's first refresh skips the rescale.
   if (__ballot(lmax > st.m + kRescaleSlack)) {
-    float mt = fmaxf(lmax, __shfl_xor(lmax, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mt = group_max(lmax);
     const float mnew = fmaxf(st.m, mt);
-    const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
-    st.l *= alpha;
+    if (__ballot(st.m != kMaxSentinel)) {
+      const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
+      st.l *= alpha;
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) st.O[jj] = st.O[jj] * alpha;
-    resc(alpha);
+      for (int jj = 0; jj < 8; ++jj) st.O[jj] = st.O[jj] * alpha;
+      resc(alpha);
+    }
     st.m = mnew;
   }
 
@@ -469,13 +495,14 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
 #pragma unroll
   for (int j = 1; j < 8; ++j) lmax = fmaxf(lmax, x[j]);
   if (__ballot(lmax > st.m + slack)) {
-    float mt = fmaxf(lmax, __shfl_xor(lmax, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mt = group_max(lmax);
     const float mnew = fmaxf(st.m, mt);
-    const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);   // head n (lane layout)
-    st.l *= alpha;
-    if (MIXED) st.fs *= alpha;
-    q_state_rescale(qs, alpha, lane);
+    if (__ballot(st.m != kMaxSentinel)) {   // else nothing accumulated yet
+      const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);   // head n (lane layout)
+      st.l *= alpha;
+      if (MIXED) st.fs *= alpha;
+      q_state_rescale(qs, alpha, lane);
+    }
     st.m = mnew;
   }
   float pf[8];
