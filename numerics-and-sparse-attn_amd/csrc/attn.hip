@@ -322,6 +322,37 @@ __host__ __device__ inline SlotRanges sparse_ranges(int64_t seq_len, int32_t win
   return R;
 }
 
+// The fp16 queue of one unit: wave w takes items w and w + kWaves at launch
+// and, when the queue is longer than 2 kWaves, claims more from the counter.
+// A wave with at most one item issues only that item's loads: while the
+// CU's memory pipeline is full every load instruction costs issue time,
+// dummies included.
+template <class Items, class Sync>
+__device__ __forceinline__ void f16_queue(const AttnCommon& P, const Items& it, const SlotRanges& R,
+                                          int wave, int lane, int* ctr, Sync&& sync, WaveState& st) {
+  StepCtx c;
+  const bool dyn = it.n > 2 * kWaves;
+  if (!dyn && wave + kWaves >= it.n) {
+    typename Items::Raw X;
+    const bool has = wave < it.n;
+    if (has) it.load(wave, X, lane);
+    sync(c, false);
+    c.R = R;
+    if (has) it.step(wave, X, st, c);
+  } else {
+    Ring<Items> ring;
+    ring_begin(it, ring, wave, wave + kWaves, lane);
+    sync(c, dyn);
+    c.R = R;
+    if (dyn)
+      ring_run_dynamic(it, ring, ctr, st, c);
+    else
+      ring_run_static(it, ring, st, c);
+  }
+  publish_ml(P, st, c.lds, lane, wave);
+  publish_f(P, st, c.slot, lane);
+}
+
 // fp16 rows: the dense cache [B, KVH, L, 128] or the compacted sparse cache
 // [B, KVH, sink+window, 128]; slot == row.
 struct F16Src {
@@ -351,16 +382,7 @@ struct F16Src {
     // (1.8% at L = 163840).
     if (it.n > 0) it.rot = (int)((uint64_t)pair % (uint64_t)it.n);
     it.R = P.R;
-    Ring<F16Items> ring;
-    ring_begin(it, ring, wave, wave + kWaves, lane);
-    StepCtx c;
-    sync(c, it.n > 2 * kWaves);
-    if (it.n > 2 * kWaves)
-      ring_run_dynamic(it, ring, ctr, st, c);
-    else
-      ring_run_static(it, ring, st, c);
-    publish_ml(P, st, c.lds, lane, wave);
-    publish_f(P, st, c.slot, lane);
+    f16_queue(P, it, P.R, wave, lane, ctr, sync, st);
   }
 };
 
@@ -470,17 +492,7 @@ struct PagedSrc {
     it.tile0 = split * P.tiles_per_split;
     it.n = max(0, min(P.tiles_per_split, tiles - it.tile0));
     it.R = R;
-    Ring<PagedItems> ring;
-    ring_begin(it, ring, wave, wave + kWaves, lane);
-    StepCtx c;
-    sync(c, it.n > 2 * kWaves);
-    c.R = R;
-    if (it.n > 2 * kWaves)
-      ring_run_dynamic(it, ring, ctr, st, c);
-    else
-      ring_run_static(it, ring, st, c);
-    publish_ml(P, st, c.lds, lane, wave);
-    publish_f(P, st, c.slot, lane);
+    f16_queue(P, it, R, wave, lane, ctr, sync, st);
   }
 };
 
@@ -601,22 +613,30 @@ struct KiviSrcBase {
       rit.R = R;
       bool has_q = false;
       if (hand && rw < extra) {
-        Ring<QItems<false>> qring;
-        ring_begin(qonly, qring, nqw + rw, qonly.n, lane);
+        QTileRaw E;
+        qonly.load(nqw + rw, E, lane);
         sync(c, true);
         if constexpr (MODE != kOneRange) c.R = R;
-        ring_run_static(qonly, qring, qref, c);
+        qonly.step(nqw + rw, E, qref, c);
         publish_ml(P, st, c.lds, lane, wave);
         publish_q<false>(qs, c.slot, lane);
         return;
       }
       if (hand) {
-        // loads issued after the barrier, behind every quantized tile's
+        // loads issued after the barrier, behind every quantized tile's.
+        // Only real tiles are loaded: while the CU's memory pipeline is
+        // full, every load instruction costs issue time, dummies included.
         sync(c, true);
         if constexpr (MODE != kOneRange) c.R = R;
-        Ring<F16Items> rring;
-        ring_begin(rit, rring, rw, rw - extra < extra ? rw - extra : rit.n, lane);
-        ring_run_static(rit, rring, st, c);
+        if (rw - extra < extra) {
+          Ring<F16Items> rring;
+          ring_begin(rit, rring, rw, rw - extra, lane);
+          ring_run_static(rit, rring, st, c);
+        } else {
+          F16Raw X;
+          rit.load(rw, X, lane);
+          rit.step(rw, X, st, c);
+        }
       } else if (nqw > 0) {
         // one extra quantized tile (if there is one) and one residual tile.
         // The residual tile's loads are issued after the workgroup barrier,
@@ -660,6 +680,11 @@ struct KiviSrcBase {
       publish_f(P, st, c.slot, lane);
       if (has_q) publish_q<true>(qs, c.slot, lane);
     } else {
+      // Both entries are loaded even when the second is past the queue:
+      // those loads return nothing but hold the quantized waves a little
+      // longer before the barrier, which keeps the residual tiles' loads
+      // behind every quantized tile's (measured: skipping them costs about
+      // 0.5 us per step at window 256..288).
       Ring<QItems<false>> qring;
       ring_begin(qonly, qring, qw, qw + nqw + nrw, lane);
       sync(c, dyn || nqw > 0);
