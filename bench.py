@@ -30,7 +30,11 @@ K back-to-back calls that cycle through them in one HIP graph; the graph is
 replayed W times untimed, then once between two HIP events on the capture
 stream.  ``ms_per_step`` / ``value`` = that time / K: the steady-state cost
 of a decode step whose inputs are cold in every cache, with launches
-pipelined as in a decode loop.  ``latency_us`` is the reference harness's
+pipelined as in a decode loop.  A replay also carries a fixed cost of about
+30 us (the graph's submission) that K amortises: the default K = 400 puts it
+near 0.1 us per microsecond-scale step (at K = 50 it would add 0.6 us).  The
+millisecond-scale paths time K/5 (dense, paged), K/10 (quantize) and K/2
+(dense L=32768) steps.  ``latency_us`` is the reference harness's
 method (triton do_bench): a 1 GiB buffer write before each single call,
 events around the call; it adds the per-call dispatch latency (about 5 us
 on this system for an empty kernel).
@@ -258,7 +262,7 @@ KIVI_KEYS = ("k_residual", "v_residual",
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--paths", default="kivi,dense,sparse,quantize,sweep,stream,paged")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
