@@ -19,7 +19,9 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
             reserve the next token's ring row (quantizing a block every 32
             steps), then attend; each cache advances 32 steps, so the time
             includes one eviction per 32 steps.  Also the same loop with one
-            ring state per sequence (KiviStreamBatch: + the bookkeeping launch)
+            ring state per sequence (KiviStreamBatch.step_attend: the
+            token's row write, evictions, bookkeeping and decode in one
+            launch)
   paged     the dense L=163840 cache scattered over 16-token pages in a
             random order (vLLM's [pages, 16, KVH, D] layout), decoded through
             block tables and per-sequence lengths (paged_kernel.py)
@@ -366,23 +368,24 @@ def main():
         del caches
 
         # the same loop with one ring state per sequence (kivi_stream.
-        # KiviStreamBatch): per step the on-GPU bookkeeping launch, the
-        # evictions and the decode, every sequence active
+        # KiviStreamBatch.step_attend): per step one launch that writes each
+        # sequence's token row, quantizes the blocks due for eviction, keeps
+        # the on-GPU bookkeeping and attends, every sequence active
         from kivi_stream import KiviStreamBatch
-        batches = []
+        batches, new_kv = [], []
         for _ in range(ns):
             kc, vc = compacted(W)
             batches.append(KiviStreamBatch.from_prefill(kc, vc, W))
             del kc, vc
+            new_kv.append((randn(B, KVH, D), randn(B, KVH, D)))
 
         def bcall(i):
-            c = batches[i % ns]
-            c.reserve()
-            return c.attend(toks[i % ns][0])
+            kn, vn = new_kv[i % ns]
+            return batches[i % ns].step_attend(toks[i % ns][0], kn, vn)
 
         ms, _ = graph_time(bcall, ns, ssteps, Wu)
         out["kivi_stream_seqs_w256"] = path_record(ms, bytes_stream_step(W), ns, ssteps)
-        del batches, toks
+        del batches, toks, new_kv
 
     if "sparse" in paths:
         ns = n_sets(bytes_sparse(W))

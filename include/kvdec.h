@@ -279,6 +279,24 @@ int kvdec_kivi_stream_decode_seqs(const void* q, const void* k_ring, const void*
                                   int32_t bits, float sm_scale, void* stream);
 
 /*
+ * kvdec_kivi_stream_step_decode: kvdec_kivi_stream_step with k_new / v_new
+ * (required here) followed by kvdec_kivi_stream_decode_seqs over the
+ * stepped state, in one launch: each (b, kv) workgroup first writes its
+ * token's row and quantizes its evicted block (if any), then attends.
+ * kivi[12] as for kvdec_kivi_stream_decode (the window-old tensors are
+ * written by evictions); appended, active, arrive, plan and ring as for
+ * kvdec_kivi_stream_step, left as that call leaves them.  No counterpart
+ * in the reference, which builds its caches once (quant_kernel.py:584-622).
+ */
+int kvdec_kivi_stream_step_decode(const void* q, const void* k_new, const void* v_new,
+                                  void* k_ring, void* v_ring, void* const* kivi, void* o,
+                                  int32_t* appended, const int32_t* active, int32_t* arrive,
+                                  int32_t* plan, int32_t* ring, int64_t B, int32_t H,
+                                  int32_t KVH, int32_t sink, int32_t residual,
+                                  int32_t n_groups, int32_t ring_cap, int32_t group,
+                                  int32_t bits, float sm_scale, void* stream);
+
+/*
  * The whole KIVI cache from a compacted K/V cache in one launch.  Replaces
  * build_quantized_kv_cache (quant_kernel.py:584-622: slicing :592-593 and
  * :608-609, sink padding :602-606, four quantizer calls :611-614).

@@ -66,6 +66,9 @@ SIGNATURES = {
     "kvdec_kivi_stream_decode_seqs": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _vp, _i64,
                                                      _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                                      _vp]),
+    "kvdec_kivi_stream_step_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _vp,
+                                                     _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32,
+                                                     _i32, _i32, _i32, _i32, _f32, _vp]),
     "kvdec_build_kivi_cache": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _i64, _i32, _i32,
                                               _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_vp), _vp]),
     "kvdec_dequant_k_tile": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32,

@@ -21,6 +21,7 @@
 // fp16 tiles to other residual waves, balancing the SIMDs' VALU load.
 
 #include "kvdec_device.h"
+#include "kvdec_stream.h"
 #include "kvdec.h"
 
 using namespace kvdec;
@@ -501,13 +502,23 @@ struct PagedSrc {
 // instantiations, so the one-length kernel carries nothing of the others):
 //   kOneRange  P.R for every sequence
 //   kSeqLens   the _kv_indices rule at each sequence's own length lens[b]
+//   kSeqStep   the same ring, first advanced by one token step in the
+//              kernel's prologue (see KiviStepSrc)
 //   kSeqRings  the residual is a ring of res_rows rows whose valid rows are
 //              [start, start + count) mod res_rows, ring[b] = {start, count}
 //              (a decode-time cache; every sink and window-old slot valid)
-enum { kOneRange = 0, kSeqLens = 1, kSeqRings = 2 };
+enum { kOneRange = 0, kSeqLens = 1, kSeqRings = 2, kSeqStep = 3 };
+
+// kSeqStep: the decode-time cache's step arguments (nothing in the others).
+template <int MODE>
+struct KiviStepArgs {};
+template <>
+struct KiviStepArgs<kSeqStep> {
+  StreamArgs a;
+};
 
 template <int MODE>
-struct KiviSrcBase {
+struct KiviSrcBase : KiviStepArgs<MODE> {
   const _Float16* kres;
   const _Float16* vres;
   int res_rows;
@@ -555,6 +566,41 @@ struct KiviSrcBase {
       const int base = sink + win_tok, end = start + count;
       R = end <= res_rows ? SlotRanges{base, base + start, base + end}
                           : SlotRanges{base + end - res_rows, base + start, base + res_rows};
+    } else if constexpr (MODE == kSeqStep) {
+      // One token step of this (b, kv) head before the decode reads
+      // anything: the token's K/V row written, the ring's oldest block
+      // quantized into the oldest window-old slot when the ring fills, then
+      // a workgroup barrier (the decode below reads both).  Every wave has
+      // the sequence's count before the barrier; after it, the last of the
+      // sequence's KVH workgroups to arrive records the step and advances
+      // the count (the writes reach the next launch at the kernel boundary).
+      const StreamArgs& a = this->a;
+      const int64_t b = pair / P.KVH;
+      const int n = max((int)((cint32*)a.appended)[b], 0);
+      const bool act = !a.active || ((cint32*)a.active)[b] != 0;
+      asm volatile("" ::"s"(n), "s"((int)act));   // both loaded before the barrier
+      const RingStep rs = ring_step(n, act, a.residual, a.cap, a.nwg);
+      if (rs.row >= 0 && threadIdx.x < 2 * kRowBytes / 16) {
+        const int i = threadIdx.x % (kRowBytes / 16);
+        const bool isv = threadIdx.x >= kRowBytes / 16;
+        const u32x4 x = *reinterpret_cast<const u32x4*>((isv ? a.v_new : a.k_new) + (size_t)pair * kHeadDim + 8 * i);
+        *reinterpret_cast<u32x4*>((isv ? a.v_ring : a.k_ring) + ((size_t)pair * a.cap + rs.row) * kHeadDim + 8 * i) = x;
+      }
+      if (a.nwg > 0 && rs.blk >= 0) evict_block(a, pair, rs.blk, rs.slot, threadIdx.x, kThreads);
+      __syncthreads();
+      // the workgroup's last thread (its wave writes no row and evicts less)
+      if (threadIdx.x == kThreads - 1 && atomicAdd(a.arrive + b, 1) == P.KVH - 1) {
+        a.arrive[b] = 0;
+        a.appended[b] = n + (act ? 1 : 0);
+        a.plan[3 * b] = rs.row;
+        a.plan[3 * b + 1] = rs.blk;
+        a.plan[3 * b + 2] = rs.blk >= 0 ? rs.slot : -1;
+        a.ring[2 * b] = rs.start;
+        a.ring[2 * b + 1] = rs.count;
+      }
+      const int base = sink + win_tok, end = rs.start + rs.count;
+      R = end <= res_rows ? SlotRanges{base, base + rs.start, base + end}
+                          : SlotRanges{base + end - res_rows, base + rs.start, base + res_rows};
     }
     QRegion S = sinkq, Wq = winq;
     S.kp += (size_t)pair * 8 * kHeadDim;
@@ -702,6 +748,9 @@ struct KiviSrcBase {
 struct KiviSrc : KiviSrcBase<kOneRange> {};
 struct KiviVarSrc : KiviSrcBase<kSeqLens> {};
 struct KiviRingSrc : KiviSrcBase<kSeqRings> {};
+// The decode-time cache with one ring state per sequence, stepped by one
+// token in the same launch (kvdec_kivi_stream_step_decode).
+struct KiviStepSrc : KiviSrcBase<kSeqStep> {};
 
 template <class Src>
 __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) {
@@ -711,12 +760,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) 
   // used, which would otherwise cost a cache miss per line in series.
   {
     constexpr int kArgLines = (int)(sizeof(AttnCommon) + sizeof(Src) + 63) / 64;
-    static_assert(kArgLines <= 5, "kernel arguments span more lines than are touched");
+    static_assert(kArgLines <= 6, "kernel arguments span more lines than are touched");
     const cint32* ka = (const cint32*)__builtin_amdgcn_kernarg_segment_ptr();
-    int32_t x[5];
+    int32_t x[6];
 #pragma unroll
-    for (int i = 0; i < 5; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
-    asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]));
+    for (int i = 0; i < 6; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
+    asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]), "s"(x[5]));
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1000,6 +1049,79 @@ int stream_decode(const void* q, const void* k_ring, const void* v_ring, const v
   return launch_attn(P, S1, true, 0, st);
 }
 
+// One token step of the per-sequence decode-time cache and the decode over
+// the stepped state, in one launch.
+int stream_step_decode(const void* q, const void* k_new, const void* v_new, void* k_ring, void* v_ring,
+                       void* const* kivi, void* o, int32_t* appended, const int32_t* active,
+                       int32_t* arrive, int32_t* plan, int32_t* ring, int64_t B, int32_t H,
+                       int32_t KVH, int32_t sink, int32_t residual, int32_t n_groups,
+                       int32_t ring_cap, int32_t group, int32_t bits, float sm_scale, void* stream) {
+  if (!q || !k_new || !v_new || !k_ring || !v_ring || !kivi || !o || !appended || !arrive || !plan ||
+      !ring)
+    return KVDEC_E_NULL;
+  if (bits != 2) return KVDEC_E_BITS;
+  if (group != 32) return KVDEC_E_UNSUPPORTED;
+  int rc = check_heads(B, H, KVH, kHeadDim);
+  if (rc) return rc;
+  if (sink < 1 || sink > group || n_groups < 0) return KVDEC_E_WINDOW;
+  if (residual < group || residual % group != 0 || ring_cap != residual + group) return KVDEC_E_WINDOW;
+  for (int i = 0; i < 6; ++i)
+    if (!kivi[i]) return KVDEC_E_NULL;
+  if (n_groups > 0)
+    for (int i = 6; i < 12; ++i)
+      if (!kivi[i]) return KVDEC_E_NULL;
+  const int64_t win_tok = (int64_t)n_groups * group;
+  if ((int64_t)ring_cap * kRowBytes >= ((int64_t)1 << 31) || win_tok * kHeadDim >= ((int64_t)1 << 31))
+    return KVDEC_E_SHAPE;
+
+  AttnCommon P{};
+  P.q = static_cast<const _Float16*>(q);
+  P.o = static_cast<_Float16*>(o);
+  P.ws = nullptr;
+  P.pairs = B * KVH;
+  P.H = H;
+  P.KVH = KVH;
+  P.G = H / KVH;
+  P.n_tiles = (int)(1 + n_groups + ring_cap / kTile);
+  P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
+
+  auto u8 = [&](int i) { return static_cast<uint8_t*>(kivi[i]); };
+  auto f16 = [&](int i) { return static_cast<_Float16*>(kivi[i]); };
+  KiviStepSrc S{};
+  S.kres = static_cast<const _Float16*>(k_ring);
+  S.vres = static_cast<const _Float16*>(v_ring);
+  S.res_rows = ring_cap;
+  S.sinkq = QRegion{u8(0), f16(1), f16(2), u8(3), f16(4), f16(5)};
+  S.winq = n_groups > 0 ? QRegion{u8(6), f16(7), f16(8), u8(9), f16(10), f16(11)} : S.sinkq;
+  S.sink = sink;
+  S.win_tok = (int)win_tok;
+  S.nwt = n_groups;
+  StreamArgs& a = S.a;
+  a.k_new = static_cast<const _Float16*>(k_new);
+  a.v_new = static_cast<const _Float16*>(v_new);
+  a.k_ring = static_cast<_Float16*>(k_ring);
+  a.v_ring = static_cast<_Float16*>(v_ring);
+  if (n_groups > 0) {
+    a.kp = u8(6);
+    a.ks = f16(7);
+    a.kz = f16(8);
+    a.vp = u8(9);
+    a.vs = f16(10);
+    a.vz = f16(11);
+  }
+  a.appended = appended;
+  a.active = active;
+  a.arrive = arrive;
+  a.plan = plan;
+  a.ring = ring;
+  a.D = kHeadDim;
+  a.cap = ring_cap;
+  a.nwg = n_groups;
+  a.KVH = KVH;
+  a.residual = residual;
+  return launch_attn(P, S, true, 0, static_cast<hipStream_t>(stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -1219,6 +1341,18 @@ int kvdec_kivi_stream_decode_seqs(const void* q, const void* k_ring, const void*
   if (!ring) return KVDEC_E_NULL;
   return stream_decode(q, k_ring, v_ring, kivi, o, ring, B, H, KVH, sink, n_groups, ring_cap, 0,
                        ring_cap, group, bits, sm_scale, stream);
+}
+
+int kvdec_kivi_stream_step_decode(const void* q, const void* k_new, const void* v_new,
+                                  void* k_ring, void* v_ring, void* const* kivi, void* o,
+                                  int32_t* appended, const int32_t* active, int32_t* arrive,
+                                  int32_t* plan, int32_t* ring, int64_t B, int32_t H, int32_t KVH,
+                                  int32_t sink, int32_t residual, int32_t n_groups,
+                                  int32_t ring_cap, int32_t group, int32_t bits, float sm_scale,
+                                  void* stream) {
+  return stream_step_decode(q, k_new, v_new, k_ring, v_ring, kivi, o, appended, active, arrive, plan,
+                            ring, B, H, KVH, sink, residual, n_groups, ring_cap, group, bits, sm_scale,
+                            stream);
 }
 
 }  // extern "C"

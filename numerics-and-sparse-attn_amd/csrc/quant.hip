@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "kvdec_device.h"
+#include "kvdec_stream.h"
 #include "kvdec.h"
 
 using namespace kvdec;
@@ -85,81 +86,6 @@ __device__ __forceinline__ void minmax_h2(const uint32_t* w, half2v& mn, half2v&
     mn = __builtin_elementwise_min(mn, v);
     mx = __builtin_elementwise_max(mx, v);
   }
-}
-
-// Scale and zero-point of one group (float32, reference formula).
-__device__ __forceinline__ void group_params(float mn, float mx, float& s, float& z) {
-  s = (mx - mn) / 3.0f;
-  s = (s == 0.0f) ? 1.0f : s;
-  z = floorf(-mn / s + 0.5f);
-}
-
-// Per-group constants of the code computation.
-struct QParams {
-  float s, y, z;   // scale, fl32(1 / s), zero
-  double rinv;     // RN64(1 / s), slow path
-  bool fast;
-};
-
-__device__ __forceinline__ QParams make_params(float mn, float mx) {
-  QParams q;
-  group_params(mn, mx, q.s, q.z);
-  q.fast = q.s >= 0x1p-40f && q.s <= 0x1p100f;
-  q.y = 1.0f / q.s;
-  q.rinv = 1.0 / (double)q.s;
-  return q;
-}
-
-// clamp(floor(fl32(x / s) + 0.5) + z, 0, 3) as a float (see file header).
-// E is float or _Float16.  q0 is formed as fma(x, y, +0), equal to fl32(x * y)
-// up to the sign of a zero (which cannot change a code), so that a 16-bit x
-// enters both FMAs unconverted.  The slow path converts x to double
-// directly, which keeps the two paths from sharing a converted copy of x.
-template <bool FAST, typename E>
-__device__ __forceinline__ float quant_code(E x, const QParams& q) {
-  float qv;
-  if (FAST) {
-    const float q0 = __builtin_fmaf((float)x, q.y, 0.0f);
-    const float r = __builtin_fmaf(-q0, q.s, (float)x);
-    qv = __builtin_fmaf(r, q.y, q0);
-  } else {
-    qv = (float)((double)x * q.rinv);
-  }
-  const float c = floorf(qv + 0.5f) + q.z;
-  return fminf(fmaxf(c, 0.0f), 3.0f);
-}
-
-// Replace byte `b` of `w` by the code c (an integer-valued float in [0, 3]).
-__device__ __forceinline__ uint32_t put_code(float c, uint32_t b, uint32_t w) {
-  return __builtin_amdgcn_cvt_pk_u8_f32(c, b, w);
-}
-
-// One 32-value group (x in group order) quantized by one thread: byte b of
-// the result holds the codes of x[4b .. 4b+3], LSB first (the K and V
-// packings differ only in where those 8 bytes go).
-__device__ __forceinline__ u32x2 quant_group(const float (&x)[32], QParams& q) {
-  float mn = x[0], mx = x[0];
-#pragma unroll
-  for (int i = 1; i < 32; ++i) {
-    mn = fminf(mn, x[i]);
-    mx = fmaxf(mx, x[i]);
-  }
-  q = make_params(mn, mx);
-  u32x2 out;
-#pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float c = q.fast ? quant_code<true>(x[16 * w + 4 * b + j], q)
-                               : quant_code<false>(x[16 * w + 4 * b + j], q);
-        word |= (uint32_t)c << (8 * b + 2 * j);
-      }
-    out[w] = word;
-  }
-  return out;
 }
 
 // K: one lane owns two adjacent channels of one 32-token group; a wave owns
@@ -447,96 +373,6 @@ __global__ __launch_bounds__(256) void dequant_v_tile_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// Decode-time KIVI cache: append one token per (b, kv) head to the fp16
-// residual ring and, when the ring holds a full group more than the
-// residual, quantize its oldest 32-row block into a window-old group slot.
-// One workgroup per (b, kv) head.
-// ---------------------------------------------------------------------------
-struct StreamArgs {
-  const _Float16* k_new;   // [pairs][D]
-  const _Float16* v_new;
-  _Float16* k_ring;        // [pairs][cap][D]
-  _Float16* v_ring;
-  uint8_t* kp;             // [pairs][nwg * group / 4][D]
-  _Float16* ks;            // [pairs][nwg][D]
-  _Float16* kz;
-  uint8_t* vp;             // [pairs][nwg * group][D / 4]
-  _Float16* vs;            // [pairs][nwg * group][D / group]
-  _Float16* vz;
-  // per-sequence bookkeeping (all null for one shared ring state)
-  int32_t* appended;       // [B] tokens appended since each sequence's prefill
-  const int32_t* active;   // [B] or null (all)
-  int32_t* arrive;         // [B] workgroups done this step (0 between launches)
-  int32_t* plan;           // [B][3] {row, evict block, evict slot} taken this step
-  int32_t* ring;           // [B][2] {start, count} after this step
-  int D, cap, row, blk, slot, nwg, KVH, residual;
-};
-
-// Ring bookkeeping of one sequence of a decode-time KIVI cache.  The state
-// after n appended tokens is fixed by n: n / 32 evictions, so the residual
-// ring holds rows [start, start + count) mod cap with start = 32 (n / 32)
-// mod cap and count = residual + n mod 32, and the oldest window-old group
-// sits in slot (n / 32) mod n_groups.  An active step takes row (start +
-// count) mod cap; when that fills the ring, its oldest 32-row block is
-// quantized into the oldest group's slot.  Returns the step ({row, block,
-// slot}, -1 = none) and the state after it.
-struct RingStep {
-  int row, blk, slot, start, count;
-};
-
-__device__ __forceinline__ RingStep ring_step(int n, bool act, int residual, int cap, int ngroups) {
-  const int e = n / kGroup;
-  RingStep r{-1, -1, -1, (int)(((int64_t)kGroup * e) % cap), residual + n % kGroup};
-  if (act) {
-    r.row = (r.start + r.count) % cap;
-    if (r.count + 1 == cap) {
-      r.blk = r.start / kGroup;
-      r.slot = ngroups > 0 ? e % ngroups : -1;
-      r.start = (r.start + kGroup) % cap;
-      r.count = residual;
-    } else {
-      r.count += 1;
-    }
-  }
-  return r;
-}
-
-// Quantize ring rows [32 blk, +32) of one (b, kv) head into window-old slot
-// `slot` (K per channel, V per token, the quantizers' exact formulas).
-__device__ __forceinline__ void evict_block(const StreamArgs& a, int64_t pair, int blk, int slot) {
-  const int D = a.D;
-  const size_t blk0 = (size_t)pair * a.cap + (size_t)blk * kGroup;   // first ring row of the block
-  const size_t g = (size_t)pair * a.nwg + slot;
-  // K: one thread per channel, its 32 tokens (per-channel group)
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float x[kGroup];
-#pragma unroll
-    for (int t = 0; t < kGroup; ++t) x[t] = (float)a.k_ring[(blk0 + t) * D + d];
-    QParams q;
-    const u32x2 c = quant_group(x, q);
-#pragma unroll
-    for (int p = 0; p < kGroup / 4; ++p) a.kp[(g * (kGroup / 4) + p) * D + d] = (uint8_t)(c[p >> 2] >> (8 * (p & 3)));
-    a.ks[g * D + d] = (_Float16)q.s;
-    a.kz[g * D + d] = (_Float16)q.z;
-  }
-  // V: one thread per (token, 32-channel group)
-  const int ng = D / kGroup;
-  for (int u = threadIdx.x; u < kGroup * ng; u += blockDim.x) {
-    const int t = u / ng, cg = u % ng;
-    const _Float16* src = a.v_ring + (blk0 + t) * D + cg * kGroup;
-    float x[kGroup];
-#pragma unroll
-    for (int i = 0; i < kGroup; ++i) x[i] = (float)src[i];
-    QParams q;
-    const u32x2 c = quant_group(x, q);
-    const size_t tok = g * kGroup + t;
-    *reinterpret_cast<u32x2*>(a.vp + tok * (D / 4) + cg * (kGroup / 4)) = c;
-    a.vs[tok * ng + cg] = (_Float16)q.s;
-    a.vz[tok * ng + cg] = (_Float16)q.z;
-  }
-}
-
 __global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
   const int64_t pair = blockIdx.x;
   const int D = a.D;
@@ -560,7 +396,7 @@ __global__ __launch_bounds__(256) void stream_append_kernel(StreamArgs a) {
       a.k_ring[((size_t)pair * a.cap + row) * D + i] = a.k_new[(size_t)pair * D + i];
       a.v_ring[((size_t)pair * a.cap + row) * D + i] = a.v_new[(size_t)pair * D + i];
     }
-  if (blk >= 0) evict_block(a, pair, blk, slot);
+  if (blk >= 0) evict_block(a, pair, blk, slot, threadIdx.x, blockDim.x);
   if (a.appended) {
     // the last of the sequence's KVH workgroups to arrive records the step
     // and advances the count.  Every workgroup's threads have consumed their

@@ -206,7 +206,8 @@ class KiviStreamBatch:
     on.  The bookkeeping lives on the GPU (a token count per sequence, from
     which each step's ring row, eviction and ring state follow, kept by the
     append kernel itself), so a step is two launches and no host round
-    trip: the step (append, quantize-on-evict, bookkeeping) and attend.  Each sequence's state equals
+    trip: the step (append, quantize-on-evict, bookkeeping) and attend, or
+    one (step_attend).  Each sequence's state equals
     a KiviStreamCache of that sequence alone after the same appends."""
 
     def __init__(self, tensors, window, sink, residual):
@@ -280,6 +281,37 @@ class KiviStreamBatch:
         v_ring[b, :, row[b]].  Evictions due at this token are enqueued here."""
         self._step(None, None, active)
         return self.plan[:, 0]
+
+    def step_attend(self, q, k_new, v_new, active=None, sm_scale=None):
+        """append(k_new, v_new, active) then attend(q), in one launch (each
+        (b, kv) workgroup writes its token's row and quantizes its evicted
+        block before it attends); returns o [B, H, D].  Leaves the cache as
+        the two calls do."""
+        B, KVH, D = self.shape
+        k_new = k_new.reshape(B, KVH, D).contiguous()
+        v_new = v_new.reshape(B, KVH, D).contiguous()
+        _checks.require_gpu_tensor("q", q, ndim=3)
+        _checks.require_shape("q", q, (B, q.shape[1], D))
+        _checks.require_gpu_tensor("k_new", k_new, ndim=3)
+        _checks.require_gpu_tensor("v_new", v_new, ndim=3)
+        _checks.require_same_device(("q", q), ("k_new", k_new), ("v_new", v_new), ("k_ring", self.t["k_ring"]))
+        act = None
+        if active is not None:
+            act = active.to(device=self.appended.device, dtype=torch.int32).contiguous()
+            _checks.require_gpu_tensor("active", act, dtypes=(torch.int32,), ndim=1)
+            _checks.require_shape("active", act, (B,))
+        o = torch.empty_like(q)
+        if sm_scale is None:
+            sm_scale = D_HEAD**-0.5
+        names = _SINK_KEYS + _WIN_KEYS
+        arr = (K._vp * 12)(*[K.ptr(self.t[n]) if self.t[n].numel() else None for n in names])
+        rc = K.lib.kvdec_kivi_stream_step_decode(
+            K.ptr(q), K.ptr(k_new), K.ptr(v_new), K.ptr(self.t["k_ring"]), K.ptr(self.t["v_ring"]), arr,
+            K.ptr(o), K.ptr(self.appended), K.ptr(act), K.ptr(self.arrive), K.ptr(self.plan),
+            K.ptr(self.ring), B, q.shape[1], KVH, self.sink, self.residual, self.n_groups, self.cap,
+            GROUP_SIZE, QUANT_BITS, float(sm_scale), K.stream_of(q))
+        K.check(rc, "KiviStreamBatch.step_attend")
+        return o
 
     def attend(self, q, sm_scale=None):
         """Decode attention of q [B, H, D] fp16 over each sequence's cache."""

@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 19
+    assert len(funcs) == 20
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -325,6 +325,33 @@ def test_stream_seqs_validation():
     assert dec(FAKE, FAKE, FAKE, arr, FAKE, FAKE, 4, 64, 8, 0, 4, 160, 32, 2, 0.088, None) == E["WINDOW"]
     assert dec(FAKE, FAKE, FAKE, arr, FAKE, FAKE, 4, 64, 8, 4, 4, 48, 32, 2, 0.088, None) == E["WINDOW"]
     assert dec(FAKE, FAKE, FAKE, arr, FAKE, FAKE, 4, 60, 8, 4, 4, 160, 32, 2, 0.088, None) == E["SHAPE"]
+
+
+def test_stream_step_decode_validation():
+    L = K.lib
+
+    def call(**kw):
+        a = dict(q=FAKE, kn=FAKE, vn=FAKE, kr=FAKE, vr=FAKE, kivi=[0x1000] * 12, o=FAKE, app=FAKE,
+                 act=None, arr=FAKE, plan=FAKE, ring=FAKE, B=4, H=64, KVH=8, sink=4, R=128, ng=4,
+                 cap=160, group=32, bits=2)
+        a.update(kw)
+        arr = (K._vp * 12)(*a["kivi"])
+        return L.kvdec_kivi_stream_step_decode(a["q"], a["kn"], a["vn"], a["kr"], a["vr"], arr, a["o"],
+                                               a["app"], a["act"], a["arr"], a["plan"], a["ring"], a["B"],
+                                               a["H"], a["KVH"], a["sink"], a["R"], a["ng"], a["cap"],
+                                               a["group"], a["bits"], 0.088, None)
+
+    assert call(kn=None) == E["NULL"]                   # the token's K / V are required here
+    assert call(vn=None) == E["NULL"]
+    assert call(app=None) == E["NULL"]
+    assert call(ring=None) == E["NULL"]
+    assert call(kivi=[0x1000] * 6 + [0] * 6) == E["NULL"]   # window-old tensors with ng > 0
+    assert call(bits=4) == E["BITS"]
+    assert call(group=64) == E["UNSUPPORTED"]
+    assert call(H=60) == E["SHAPE"]
+    assert call(sink=0) == E["WINDOW"]
+    assert call(cap=192) == E["WINDOW"]
+    assert call(R=100, cap=132) == E["WINDOW"]
 
 
 def _build(**kw):

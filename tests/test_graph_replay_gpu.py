@@ -137,3 +137,46 @@ def test_graph_stream_batch_step(device):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(host(out), want, err_msg=str(i))
     np.testing.assert_array_equal(host(graphed.appended), host(eager.appended))
+
+
+def test_graph_stream_step_attend(device):
+    """A captured step_attend (one launch: row write, eviction, bookkeeping,
+    decode) advances the cache on every replay: 40 replays (crossing an
+    eviction) equal 40 eager calls on an identical cache."""
+    from kivi_stream import KiviStreamBatch
+    B, H, KVH, D, W = 3, 16, 2, 128, 256
+    L0 = S + W + 5
+    gen = torch.Generator(device=device).manual_seed(4)
+    k = torch.randn(B, KVH, L0, D, generator=gen, device=device, dtype=torch.float16)
+    v = torch.randn(B, KVH, L0, D, generator=gen, device=device, dtype=torch.float16)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    kn = torch.randn(B, KVH, D, generator=gen, device=device, dtype=torch.float16)
+    vn = torch.randn(B, KVH, D, generator=gen, device=device, dtype=torch.float16)
+    active = torch.tensor([1, 0, 1], dtype=torch.int32, device=device)
+    eager = KiviStreamBatch.from_prefill(k, v, W)
+    graphed = KiviStreamBatch.from_prefill(k, v, W)
+    warm = KiviStreamBatch.from_prefill(k, v, W)
+    say("graph stream step_attend")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        warm.step_attend(q, kn, vn, active)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = graphed.step_attend(q, kn, vn, active)   # captured, not run
+    for i in range(40):
+        want = host(eager.step_attend(q, kn, vn, active))
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(out), want, err_msg=str(i))
+    np.testing.assert_array_equal(host(graphed.ring), host(eager.ring))
+    np.testing.assert_array_equal(host(graphed.appended), host(eager.appended))
+    for name in eager.t:
+        if name in ("k_ring", "v_ring"):   # free rows hold whatever the allocation held
+            for b, (start, count) in enumerate(host(eager.ring)):
+                rows = [(start + i) % eager.cap for i in range(count)]
+                np.testing.assert_array_equal(host(graphed.t[name][b])[:, rows], host(eager.t[name][b])[:, rows])
+        else:
+            np.testing.assert_array_equal(host(graphed.t[name]), host(eager.t[name]), err_msg=name)

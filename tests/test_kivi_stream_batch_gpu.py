@@ -133,3 +133,45 @@ def test_batch_reserve_equals_append(device):
         np.testing.assert_array_equal(host(a.t[name]), host(b.t[name]), err_msg=name)
     np.testing.assert_array_equal(host(a.ring), host(b.ring))
     np.testing.assert_array_equal(host(a.attend(q)), host(b.attend(q)))
+
+
+@pytest.mark.parametrize("W", [256, 1024])
+def test_step_attend_equals_append_then_attend(W, device):
+    """step_attend (one launch: each workgroup writes its token's row,
+    quantizes its evicted block, then attends) against append followed by
+    attend on an identical cache, over 75 steps with random active masks
+    (every sequence crosses at least one eviction): the same outputs (W=256
+    bit for bit; W=1024's dynamic work queue may sum in another order, so
+    one fp16 ulp), and every cache tensor and the bookkeeping bit for bit."""
+    from kivi_stream import KiviStreamBatch
+    B, H, KVH, D = 5, 16, 2, 128
+    L0, steps = S + W + 9, 75
+    gen = torch.Generator(device=device).manual_seed(100 + W)
+    k = torch.randn(B, KVH, L0, D, generator=gen, device=device, dtype=torch.float16)
+    v = torch.randn(B, KVH, L0, D, generator=gen, device=device, dtype=torch.float16)
+    kn = torch.randn(steps, B, KVH, D, generator=gen, device=device, dtype=torch.float16)
+    vn = torch.randn(steps, B, KVH, D, generator=gen, device=device, dtype=torch.float16) * 3
+    q = torch.randn(steps, B, H, D, generator=gen, device=device, dtype=torch.float16)
+    two = KiviStreamBatch.from_prefill(k, v, W)
+    one = KiviStreamBatch.from_prefill(k, v, W)
+    rng = np.random.default_rng(W)
+    say(f"stream step_attend W={W}")
+    for i in range(steps):
+        active = torch.from_numpy(rng.random(B) < 0.8).to(device)
+        two.append(kn[i], vn[i], active)
+        o2 = host(two.attend(q[i]))
+        o1 = host(one.step_attend(q[i], kn[i], vn[i], active))
+        if W == 256:
+            np.testing.assert_array_equal(o1, o2, err_msg=str(i))
+        else:
+            assert max_abs(o1, o2) < ATTN_TOL, i
+    for name in two.t:
+        if name in ("k_ring", "v_ring"):   # free rows hold whatever the allocation held
+            for b, (start, count) in enumerate(host(two.ring)):
+                rows = [(start + i) % two.cap for i in range(count)]
+                np.testing.assert_array_equal(host(one.t[name][b])[:, rows], host(two.t[name][b])[:, rows])
+        else:
+            np.testing.assert_array_equal(host(one.t[name]), host(two.t[name]), err_msg=name)
+    for name in ("appended", "ring", "plan", "arrive"):
+        np.testing.assert_array_equal(host(getattr(one, name)), host(getattr(two, name)), err_msg=name)
+    assert int(host(one.appended).min()) >= 32
