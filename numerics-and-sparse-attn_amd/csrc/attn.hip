@@ -31,12 +31,6 @@ namespace {
 constexpr int kWaves = 8;                        // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 
-#ifndef KVDEC_RES_FIRST
-#define KVDEC_RES_FIRST 1
-#endif
-#ifndef KVDEC_Q_SLEEP
-#define KVDEC_Q_SLEEP 0
-#endif
 
 struct AttnCommon {
   const _Float16* q;     // [B, H, 128]
@@ -640,11 +634,7 @@ struct KiviSrcBase : KiviStepArgs<MODE> {
     // carries a quantized and an fp16 step more than the others.
     const int extra = nqw > 0 && !dyn_q ? max(qit.n - nqw, 0) : 0;
     const bool hand = extra > 0 && 2 * extra <= nrw;
-#if KVDEC_RES_FIRST
-    const int rw = wave, qw = wave - nrw;
-#else
-    const int rw = wave - nqw, qw = wave;
-#endif
+    const int rw = wave, qw = wave - nrw;   // residual waves first
     StepCtx c;
     if (rw >= 0 && rw < nrw) {
       F16Items rit;
