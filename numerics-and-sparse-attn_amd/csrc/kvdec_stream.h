@@ -17,7 +17,8 @@ namespace kvdec {
 
 constexpr int kQGroup = 32;
 
-// Scale and zero-point of one group (float32, reference formula).
+// Scale and zero-point of one group (float32, the reference's formula,
+// quant_kernel.py:77-81 for K and :166-170 for V).
 __device__ __forceinline__ void group_params(float mn, float mx, float& s, float& z) {
 #pragma clang fp contract(off)
   s = (mx - mn) / 3.0f;
