@@ -4,7 +4,7 @@
                     [--paths kivi,dense,sparse,quantize,sweep,stream,paged]
                     [--no-cpu] [--no-latency]
 
-Workload (the BASELINE metric's configuration): B=32, 64 query / 8 KV heads,
+Workload (the headline metric's configuration): B=32, 64 query / 8 KV heads,
 head_dim 128, logical context L=163840, sink S=4, window W=256, KIVI residual
 R=128, fp16 inputs ~ N(0,1) from a fixed seed with 4 of the 128 K channels
 scaled x10.  A "step" is one decode call of a path over the whole batch:
