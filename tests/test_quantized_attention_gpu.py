@@ -48,6 +48,30 @@ def test_kivi_golden(device):
     assert max_abs(_attend(q, cache, 150, W), g["o_ramp"]) < ATTN_TOL
 
 
+@pytest.mark.parametrize("W", [160, 192, 224, 288, 320, 384, 448, 480])
+def test_quantized_attention_work_splits(W, device):
+    """Every static work split of the 8 waves: 1..3 window groups (the
+    quantized waves take them all), 5 (one leftover tile: a residual wave
+    steps the sink and hands its fp16 tile over), 6 (two leftovers, two
+    hand-overs), 7 (three leftovers, no hand-over), 8..11 (every residual
+    wave takes a leftover, the quantized waves a second tile); W=512 and up
+    run the dynamic queue (above).  B=8 keeps the oracle fast."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D = 8, 64, 8, 128
+    L = S + W + 77
+    gen = torch.Generator(device=device).manual_seed(1000 + W)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    say(f"kivi work split W={W}")
+    cache = build_quantized_kv_cache(kc, vc)
+    o = _attend(q, cache, L, W)
+    hc = _host_cache(cache)
+    ref = O.quantized_attention(host(q), W - R, hc, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+    assert_nearly_rounded(o, ref)
+
+
 @pytest.mark.parametrize("W", [128, 256, 512, 1024, 4096, 8192])
 def test_quantized_attention_steady_state(W, device):
     """Reference case (seed 3 analogue, W in {256, 512, 8192}) plus W = R and
