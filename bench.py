@@ -1,7 +1,7 @@
 """Decode-attention benchmark on one MI355X: prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--paths kivi,dense,sparse,quantize,sweep,stream,paged]
+                    [--paths kivi,sweep,dense,sparse,quantize,stream,paged,grid]
                     [--no-cpu] [--no-latency]
 
 Workload (the headline metric's configuration): B=32, 64 query / 8 KV heads,
@@ -10,46 +10,56 @@ R=128, fp16 inputs ~ N(0,1) from a fixed seed with 4 of the 128 K channels
 scaled x10.  A "step" is one decode call of a path over the whole batch:
 
   kivi      fused sink+window(W=256)+KIVI-2bit decode (the headline ``value``)
+  sweep     the fused decode at W = 32, 1024 and 4096 (config 5; W=32 < R,
+            which the reference leaves undefined, keeps the window fp16)
   dense     dense GQA decode over all 163840 tokens (and L=32768, config 2)
   sparse    fp16 sink+window(W=256) decode (config 3)
   quantize  KIVI quantization of the [32, 8, 163840, 128] K and V caches (config 4)
-  sweep     the fused decode at W = 32, 1024 and 4096 (config 5; W=32 < R,
-            which the reference leaves undefined, keeps the window fp16)
   stream    a decode loop on the streaming KIVI cache (kivi_stream.py, W=256):
             reserve the next token's ring row (quantizing a block every 32
-            steps), then attend; each cache advances 32 steps, so the time
-            includes one eviction per 32 steps.  Also the same loop with one
-            ring state per sequence (KiviStreamBatch.step_attend: the
-            token's row write, evictions, bookkeeping and decode in one
-            launch)
+            steps), then attend; also the same loop with one ring state per
+            sequence (KiviStreamBatch.step_attend: the token's row write,
+            evictions, bookkeeping and decode in one launch)
   paged     the dense L=163840 cache scattered over 16-token pages in a
             random order (vLLM's [pages, 16, KVH, D] layout), decoded through
             block tables and per-sequence lengths (paged_kernel.py)
+  grid      the reference harness's sweep (benchmark.py:34-169): dense at
+            every L of CONTEXT_LENGTHS, sparse at every W of WINDOW_SIZES and
+            the fused KIVI decode at W = 32 and every W >= R, with the
+            batch-1 host CPU time beside each point.  Sparse and KIVI steps
+            read the same bytes at every L >= S + W (steady state), so they
+            are timed once per W at L = 163840.
 
-Timing.  Each path keeps several independent input sets resident in HBM
-(together >= 1 GiB, more than L2 plus the 256 MB Infinity Cache) and captures
-K back-to-back calls that cycle through them in one HIP graph; the graph is
-replayed W times untimed, then once between two HIP events on the capture
-stream.  ``ms_per_step`` / ``value`` = that time / K: the steady-state cost
-of a decode step whose inputs are cold in every cache, with launches
-pipelined as in a decode loop.  A replay also carries a fixed cost of about
-30 us (the graph's submission) that K amortises: the default K = 400 puts it
-near 0.1 us per microsecond-scale step (at K = 50 it would add 0.6 us).  The
-millisecond-scale paths time K/5 (dense, paged), K/10 (quantize) and K/2
-(dense L=32768) steps.  ``latency_us`` is the reference harness's
-method (triton do_bench): a 1 GiB buffer write before each single call,
-events around the call; it adds the per-call dispatch latency (about 5 us
-on this system for an empty kernel).
+Timing.  Each path keeps enough independent input sets resident in HBM that
+one pass over them is >= 1 GiB (more than L2 plus the 256 MB Infinity
+Cache), captures G = max(K, sets) back-to-back calls cycling through every
+set in one HIP graph, replays it untimed, then times R back-to-back replays
+(R * G >= 1000 steps for the microsecond-scale paths, R = 2 for the
+millisecond-scale ones) between two HIP events on the capture stream:
+``us_per_step`` = that time / (R * G), the steady-state cost of a decode
+step whose inputs are cold in every cache, with launches pipelined as in a
+decode loop and the graphs' submission costs spread over all R * G steps.
+``latency_us`` is the reference harness's method (triton do_bench): a 1 GiB
+buffer write before each single call, events around the call; it adds the
+per-call dispatch latency (about 5 us on this system for an empty kernel).
 
-The CPU baseline times the numpy oracle (the repository's own restatement of
-the reference's PyTorch formulas) on the host on a bounded sample of the same
-workload.
+``roofline.traffic`` is the HBM bytes per launch recorded by the rocprofv3
+FETCH_SIZE / WRITE_SIZE runs in profiles/hbm_traffic.json; each record
+names the kernel sources it was measured on (a hash), and the line reports
+null when the sources have changed since.
+
+The CPU baseline times the repository's torch restatement of the
+reference's PyTorch test oracles (oracle/torch_ref.py) on the host, float32,
+with torch's thread pool as the process finds it (OMP_NUM_THREADS; 16 on
+the GPU boxes, which is this process's CPU share there).
 """
 
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
+import math
 import os
 import sys
 import time
@@ -69,8 +79,12 @@ S, W, R = 4, 256, 128
 HBM_PEAK_GBS = 8000.0
 REF_KIVI_W256_US = 240.87          # A100 Triton, results/benchmark_results_quantized.csv:43
 METRIC = "decode-attn µs/step + achieved HBM TB/s (% of peak), B=32 L=163840 W=256"
-COLD_SET_BYTES = 1 << 30           # rotating input sets per path: at least this many bytes
-MAX_SETS = 64
+COLD_SET_BYTES = 1 << 30           # one pass over a path's input sets reads at least this
+MAX_SETS = 512
+MIN_TIMED_STEPS = 1000             # microsecond-scale paths: R * G >= this
+CONTEXT_LENGTHS = [8192, 16384, 32768, 65536, 131072, 163840]          # constants.py:18
+WINDOW_SIZES = [0, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384]
+KERNEL_SOURCES = ("attn.hip", "kvdec_device.h", "kvdec_stream.h", "quant.hip")
 
 
 # --------------------------------------------------------------------------
@@ -112,10 +126,9 @@ def bytes_stream_step(window, residual=R):
     and write its codes and scales/zeros (K per channel, V per token).  The
     new token's K/V are written into the ring by their producer."""
     pairs = B * KVH
-    append = 0
     attend = bytes_kivi(window, residual) + pairs * 2 * 15.5 * D * 2
     evict = pairs * (2 * 32 * D * 2 + 2 * (32 * D // 4) + 2 * 2 * D + 2 * 2 * 32 * (D // 32))
-    return int(append + attend + evict / 32)
+    return int(attend + evict / 32)
 
 
 def bytes_paged(n_tok, page_size):
@@ -133,31 +146,37 @@ def bytes_quantize(n_tok):
 # timing
 # --------------------------------------------------------------------------
 
-def graph_time(call, nsets, steps, warmup):
-    """Per-step ms of `steps` back-to-back calls call(i % nsets), captured in
-    one HIP graph and replayed; returns (ms_per_step, outputs of the capture)."""
+def graph_time(call, nsets, steps, warmup, min_steps=MIN_TIMED_STEPS, replays=None):
+    """Per-step ms of back-to-back calls call(i % nsets), G = max(steps, nsets)
+    of them captured in one HIP graph (every input set once per pass), timed
+    over R back-to-back replays (R * G >= min_steps unless `replays` is
+    given).  Returns (ms_per_step, {"graph_steps": G, "replays": R})."""
+    G = max(steps, nsets)
+    Rp = replays if replays is not None else max(2, math.ceil(min_steps / G))
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        for i in range(min(3, steps)):
+        for i in range(min(3, G)):
             call(i % nsets)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    outs = []
     with torch.cuda.graph(g):
-        for i in range(steps):
-            outs.append(call(i % nsets))
+        for i in range(G):
+            call(i % nsets)
     for _ in range(max(1, warmup)):
         g.replay()
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    g.replay()
+    for _ in range(Rp):
+        g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps, outs
+    ms = e0.elapsed_time(e1) / (Rp * G)
+    del g
+    return ms, {"graph_steps": G, "replays": Rp}
 
 
 def latency_time(call, nsets, reps, flush):
@@ -178,9 +197,9 @@ def latency_time(call, nsets, reps, flush):
     return float(np.mean(per)), float(np.median(per))
 
 
-def path_record(ms, alg_bytes, nsets, steps, alg_bytes_ref=None, latency=None):
+def path_record(ms, alg_bytes, nsets, tinfo, alg_bytes_ref=None, latency=None):
     gbs = alg_bytes / (ms * 1e-3) / 1e9
-    rec = {"us_per_step": round(ms * 1e3, 3), "steps": steps, "input_sets": nsets,
+    rec = {"us_per_step": round(ms * 1e3, 3), "input_sets": nsets, **tinfo,
            "alg_bytes": int(alg_bytes), "achieved_GBs": round(gbs, 1),
            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
     if alg_bytes_ref is not None:
@@ -192,16 +211,33 @@ def path_record(ms, alg_bytes, nsets, steps, alg_bytes_ref=None, latency=None):
     return rec
 
 
+def kernel_source_hash():
+    """sha256 (first 16 hex) of the kernel sources, in a fixed order."""
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        with open(os.path.join(PKG, "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(key):
-    """HBM bytes per launch of the path's kernel, as recorded from the
-    rocprofv3 FETCH_SIZE / WRITE_SIZE runs in profiles/hbm_traffic.json
-    (calibrated against a 256 MiB copy); None when not recorded."""
+    """(HBM bytes per launch, provenance) of the path's kernel from the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs recorded in profiles/
+    hbm_traffic.json; bytes are None when nothing is recorded or the record
+    was measured on other kernel sources."""
+    src = {"file": "profiles/hbm_traffic.json", "key": key}
     try:
         with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
             rec = json.load(f).get(key)
-        return None if rec is None else int(rec["fetch_bytes_per_launch"] + rec["write_bytes_per_launch"])
-    except (OSError, ValueError, KeyError):
-        return None
+    except (OSError, ValueError):
+        rec = None
+    if rec is None:
+        return None, {**src, "status": "not recorded"}
+    src.update(commit=rec.get("commit"), recorded_source_sha16=rec.get("source_sha16"),
+               current_source_sha16=kernel_source_hash())
+    if rec.get("source_sha16") != src["current_source_sha16"]:
+        return None, {**src, "status": "stale: recorded on other kernel sources"}
+    return int(rec["fetch_bytes_per_launch"] + rec["write_bytes_per_launch"]), {**src, "status": "current"}
 
 
 def n_sets(bytes_per_set):
@@ -209,47 +245,92 @@ def n_sets(bytes_per_set):
 
 
 # --------------------------------------------------------------------------
-# CPU baseline (numpy oracle on the host)
+# CPU baseline: the torch restatement of the reference's test oracles
 # --------------------------------------------------------------------------
 
-def _blas_threads():
+def host_info():
+    model = "unknown"
     try:
-        from threadpoolctl import threadpool_info
-        n = [i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"]
-        return int(max(n)) if n else 1
-    except Exception:
-        return 1
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"cpu_model": model, "threads_used": torch.get_num_threads(), "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": affinity, "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
 
 
-def _timed(fn, min_reps=3, budget_s=10.0):
-    fn()                                   # warm-up
+def cpu_time(fn, min_reps=5, budget_s=8.0):
+    """1 warm-up call, then >= min_reps timed calls (more while within
+    budget_s, at most 30); returns (median seconds, reps)."""
+    fn()
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < min_reps or time.perf_counter() < t_end:
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < 30):
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
-            break
     return float(np.median(times)), len(times)
 
 
-def cpu_baseline_kivi(q, cache):
-    from oracle import kvdec_oracle as O
-    qh = q.cpu().numpy()
-    hc = {k: v.cpu().numpy() for k, v in cache.items()}
-    sec, reps = _timed(lambda: O.quantized_attention(qh, W - R, hc, D**-0.5, dtype=np.float32))
+def cpu_randn(*shape, seed=0):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed))
+
+
+def cpu_dense_b1(n_tok, seed=0):
+    """One sequence of the dense step on the host: (median us, reps)."""
+    from oracle import torch_ref as T
+    q = cpu_randn(1, H, D, seed=seed)
+    k = cpu_randn(1, KVH, n_tok, D, seed=seed + 1)
+    v = cpu_randn(1, KVH, n_tok, D, seed=seed + 2)
+    sec, reps = cpu_time(lambda: T.dense_attention(q, k, v, D**-0.5), min_reps=5, budget_s=2.0)
     return sec * 1e6, reps
 
 
-def cpu_baseline_dense(q, k, v, rows=1):
+def cpu_sparse(batch, window, seed=0):
+    from oracle import torch_ref as T
+    q = cpu_randn(batch, H, D, seed=seed)
+    k = cpu_randn(batch, KVH, S + window, D, seed=seed + 1)
+    v = cpu_randn(batch, KVH, S + window, D, seed=seed + 2)
+    sec, reps = cpu_time(lambda: T.sparse_attention(q, k, v, L, window, S, D**-0.5), budget_s=2.0)
+    return sec * 1e6, reps
+
+
+def cpu_kivi(q, cache, window, budget_s=2.0):
+    """The fused step's dequantize-then-attend on the host, over a cache and
+    q given as GPU tensors (copied to the host first, untimed)."""
+    from oracle import torch_ref as T
+    qh = q.cpu()
+    hc = {k: v.cpu() for k, v in cache.items()}
+    sec, reps = cpu_time(lambda: T.quantized_attention(qh, max(window - R, 0), hc, D**-0.5),
+                         budget_s=budget_s)
+    return sec * 1e6, reps
+
+
+def cpu_config1():
+    """B=1, 64q/8kv, d=128, L=8192, Q/K/V ~ N(0,1) fp32
+    from a fixed CPU seed; the torch restatement timed and its output
+    checked against the fp64 numpy oracle."""
     from oracle import kvdec_oracle as O
-    qh = q[:rows].cpu().numpy()
-    kh = k[:rows].cpu().numpy()
-    vh = v[:rows].cpu().numpy()
-    sec, reps = _timed(lambda: O.dense_attention(qh, kh, vh, D**-0.5, dtype=np.float32),
-                       min_reps=2, budget_s=6.0)
-    return sec * 1e6 * (B / rows), reps
+    from oracle import torch_ref as T
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, H, D, generator=g)
+    k = torch.randn(1, KVH, 8192, D, generator=g)
+    v = torch.randn(1, KVH, 8192, D, generator=g)
+    sec, reps = cpu_time(lambda: T.dense_attention(q, k, v, D**-0.5), min_reps=5, budget_s=3.0)
+    out = T.dense_attention(q, k, v, D**-0.5).numpy()
+    err = float(np.abs(out - O.dense_attention(q.numpy(), k.numpy(), v.numpy(), D**-0.5)).max())
+    nbytes = 2 * H * D * 4 + 2 * KVH * 8192 * D * 4
+    return {"config": "B=1 H=64 KVH=8 D=128 L=8192, fp32 N(0,1), torch.Generator seed 0",
+            "us_per_step": round(sec * 1e6, 1), "reps": reps, "alg_bytes": nbytes,
+            "achieved_GBs": round(nbytes / sec / 1e9, 2),
+            "max_abs_err_vs_fp64_oracle": err, "check": "pass" if err < 1e-4 else "FAIL"}
 
 
 # --------------------------------------------------------------------------
@@ -266,7 +347,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--paths", default="kivi,dense,sparse,quantize,sweep,stream,paged")
+    ap.add_argument("--paths", default="kivi,sweep,dense,sparse,quantize,stream,paged,grid")
+    ap.add_argument("--sweep-windows", default="32,1024,4096",
+                    help="windows of the 'sweep' path (fused KIVI decode, config 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-latency", action="store_true", help="skip the per-call latency runs")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -275,8 +358,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(run with --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU only: every GPU box of this build has one GPU and the "
+              "build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
     import dense_kernel
@@ -285,10 +368,15 @@ def main():
 
     paths = [p.strip() for p in args.paths.split(",") if p.strip()]
     K, Wu = max(1, args.steps), max(1, args.warmup)
+    Kms = max(4, min(K, 20))           # graph length of the millisecond-scale paths (2 replays)
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(0)
     outliers = torch.randperm(D, generator=torch.Generator().manual_seed(0))[:4].tolist()
     flush = None if args.no_latency else torch.empty((1 << 30) // 4, dtype=torch.int32, device=dev)
+    want_cpu = not args.no_cpu
+
+    def progress(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
     def randn(*shape):
         return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float16)
@@ -299,7 +387,8 @@ def main():
         return kc, randn(B, KVH, S + window, D)
 
     out = {}
-    cpu = None
+    cpu = {"host": host_info()} if want_cpu else None
+    head_cpu = None
 
     if args.copy_calibration:
         src = torch.ones((256 << 20) // 4, dtype=torch.int32, device=dev)
@@ -309,51 +398,68 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    def kivi_path(window, steps, name, with_cpu=False):
-        nonlocal cpu
+    def kivi_sets(window):
         ns = n_sets(bytes_kivi(window))
         sets = []
         for _ in range(ns):
             kc, vc = compacted(window)
             cache = quant_kernel.build_quantized_kv_cache(kc, vc)
             del kc, vc
-            sets.append((randn(B, H, D), [cache[k] for k in KIVI_KEYS], cache))
+            sets.append((randn(B, H, D), [cache[k] for k in KIVI_KEYS]))
+        return ns, sets
 
+    def kivi_call(sets, window):
         def call(i):
-            q, a, _ = sets[i]
+            q, a = sets[i]
             return quant_kernel.sparse_decode_attention_quantized(q, *a, seq_len=L, window=window)
+        return call
 
-        ms, _ = graph_time(call, ns, steps, Wu)
-        lat = None if flush is None else latency_time(call, ns, 50, flush)
-        out[name] = path_record(ms, bytes_kivi(window), ns, steps, bytes_kivi(window, sink_tokens=32), lat)
-        if with_cpu and not args.no_cpu:
-            us, reps = cpu_baseline_kivi(sets[0][0], sets[0][2])
-            cpu = {"value": round(us, 1), "unit": "us/step", "cores": _blas_threads(), "kind": "port",
-                   "sample": f"the full kivi_w256 step (B=32, all 256 KV heads), numpy oracle "
-                             f"dequantize-then-attend in float32, median of {reps} reps"}
-        del sets
+    def kivi_path(window, name, latency=True):
+        ns, sets = kivi_sets(window)
+        call = kivi_call(sets, window)
+        ms, ti = graph_time(call, ns, K, Wu)
+        lat = None if (flush is None or not latency) else latency_time(call, ns, 50, flush)
+        out[name] = path_record(ms, bytes_kivi(window), ns, ti, bytes_kivi(window, sink_tokens=32), lat)
+        progress(f"{name}: {out[name]['us_per_step']} us")
+        return sets
 
     if "kivi" in paths:
-        kivi_path(W, K, "kivi_w256", with_cpu=True)
+        sets = kivi_path(W, "kivi_w256")
+        if want_cpu:
+            q0, parts = sets[0]
+            us, reps = cpu_kivi(q0, dict(zip(KIVI_KEYS, parts)), W, budget_s=8.0)
+            head_cpu = {"value": round(us, 1), "unit": "us/step", "cores": cpu["host"]["threads_used"],
+                        "kind": "port",
+                        "sample": f"the whole kivi_w256 step (B=32, all 256 KV heads): oracle/torch_ref.py "
+                                  f"dequantize-then-attend in float32 (restates test_quantized_attention_"
+                                  f"correctness.py:32-61), median of {reps} reps after 1 warm-up, "
+                                  f"{cpu['host']['threads_used']} torch threads on {cpu['host']['cpu_model']}"}
+            out["kivi_w256"]["cpu_us_per_step"] = round(us, 1)
+        del sets
 
     if "sweep" in paths:
-        for w in (32, 1024, 4096):
-            kivi_path(w, K, f"kivi_w{w}")
+        for w in [int(x) for x in args.sweep_windows.split(",") if x.strip()]:
+            sets = kivi_path(w, f"kivi_w{w}")
+            if want_cpu:
+                q0, parts = sets[0]
+                us, _ = cpu_kivi(q0, dict(zip(KIVI_KEYS, parts)), w)
+                out[f"kivi_w{w}"]["cpu_us_per_step"] = round(us, 1)
+            del sets
 
     if "stream" in paths:
         # decode loop over the streaming KIVI cache (kivi_stream.py): each
         # step reserves the next token's ring row (quantizing a block into
         # the window-old ring every 32 steps) and attends; steps rotate over
         # independent caches so that every step starts cold, and each cache
-        # advances 32 tokens
-        from kivi_stream import KiviStreamCache
+        # advances 32 tokens per pass of the graph
+        from kivi_stream import KiviStreamBatch, KiviStreamCache
         ns = n_sets(bytes_stream_step(W))
         caches, toks = [], []
         for _ in range(ns):
             kc, vc = compacted(W)
             caches.append(KiviStreamCache.from_prefill(kc, vc, W))
             del kc, vc
-            toks.append((randn(B, H, D),))
+            toks.append(randn(B, H, D))
         ssteps = 32 * ns
 
         def scall(i):
@@ -361,17 +467,15 @@ def main():
             # producer (the projection), which is not part of this step
             c = caches[i % ns]
             c.reserve()
-            return c.attend(toks[i % ns][0])
+            return c.attend(toks[i % ns])
 
-        ms, _ = graph_time(scall, ns, ssteps, Wu)
-        out["kivi_stream_w256"] = path_record(ms, bytes_stream_step(W), ns, ssteps)
+        ms, ti = graph_time(scall, ns, ssteps, Wu)
+        out["kivi_stream_w256"] = path_record(ms, bytes_stream_step(W), ns, ti)
         del caches
 
-        # the same loop with one ring state per sequence (kivi_stream.
-        # KiviStreamBatch.step_attend): per step one launch that writes each
-        # sequence's token row, quantizes the blocks due for eviction, keeps
-        # the on-GPU bookkeeping and attends, every sequence active
-        from kivi_stream import KiviStreamBatch
+        # the same loop with one ring state per sequence: per step one launch
+        # that writes each sequence's token row, quantizes the blocks due for
+        # eviction, keeps the on-GPU bookkeeping and attends
         batches, new_kv = [], []
         for _ in range(ns):
             kc, vc = compacted(W)
@@ -381,10 +485,11 @@ def main():
 
         def bcall(i):
             kn, vn = new_kv[i % ns]
-            return batches[i % ns].step_attend(toks[i % ns][0], kn, vn)
+            return batches[i % ns].step_attend(toks[i % ns], kn, vn)
 
-        ms, _ = graph_time(bcall, ns, ssteps, Wu)
-        out["kivi_stream_seqs_w256"] = path_record(ms, bytes_stream_step(W), ns, ssteps)
+        ms, ti = graph_time(bcall, ns, ssteps, Wu)
+        out["kivi_stream_seqs_w256"] = path_record(ms, bytes_stream_step(W), ns, ti)
+        progress("stream done")
         del batches, toks, new_kv
 
     if "sparse" in paths:
@@ -395,33 +500,38 @@ def main():
             q, kc, vc = sets[i]
             return sparse_kernel.sparse_decode_attention(q, kc, vc, seq_len=L, window=W)
 
-        ms, _ = graph_time(call, ns, K, Wu)
+        ms, ti = graph_time(call, ns, K, Wu)
         lat = None if flush is None else latency_time(call, ns, 50, flush)
-        out["sparse_fp16_w256"] = path_record(ms, bytes_sparse(W), ns, K, latency=lat)
+        out["sparse_fp16_w256"] = path_record(ms, bytes_sparse(W), ns, ti, latency=lat)
+        if want_cpu:
+            us, reps = cpu_sparse(B, W)
+            out["sparse_fp16_w256"]["cpu_us_per_step"] = round(us, 1)
+        progress(f"sparse_fp16_w256: {out['sparse_fp16_w256']['us_per_step']} us")
         del sets
 
+    ms_warm = max(2, min(Wu, 3))
     if "quantize" in paths or "dense" in paths or "paged" in paths:
         k = randn(B, KVH, L, D)
         k[..., outliers] *= 10
         v = randn(B, KVH, L, D)
         q = randn(B, H, D)
-        dsteps = max(3, K // 5)
         if "quantize" in paths:
-            qsteps = max(3, K // 10)
-            ms, _ = graph_time(lambda i: quant_kernel.quantize_k_cache(k), 1, qsteps, 1)
-            out["quantize_k_L163840"] = path_record(ms, bytes_quantize(L), 1, qsteps)
-            ms, _ = graph_time(lambda i: quant_kernel.quantize_v_cache(v), 1, qsteps, 1)
-            out["quantize_v_L163840"] = path_record(ms, bytes_quantize(L), 1, qsteps)
+            ms, ti = graph_time(lambda i: quant_kernel.quantize_k_cache(k), 1, Kms, ms_warm, replays=2)
+            out["quantize_k_L163840"] = path_record(ms, bytes_quantize(L), 1, ti)
+            ms, ti = graph_time(lambda i: quant_kernel.quantize_v_cache(v), 1, Kms, ms_warm, replays=2)
+            out["quantize_v_L163840"] = path_record(ms, bytes_quantize(L), 1, ti)
+            progress("quantize done")
         if "dense" in paths:
-            ms, _ = graph_time(lambda i: dense_kernel.dense_decode_attention(q, k, v, seq_len=L), 1,
-                               dsteps, 1)
-            out["dense_L163840"] = path_record(ms, bytes_dense(L), 1, dsteps)
-            if not args.no_cpu:
-                us, reps = cpu_baseline_dense(q, k, v)
-                out["dense_L163840"]["cpu_baseline"] = {
-                    "value": round(us, 1), "unit": "us/step", "cores": _blas_threads(), "kind": "port",
-                    "sample": f"batch row 0 of 32 at L=163840 (numpy oracle, float32, median of "
-                              f"{reps} reps), scaled x32"}
+            ms, ti = graph_time(lambda i: dense_kernel.dense_decode_attention(q, k, v, seq_len=L), 1,
+                                Kms, ms_warm, replays=2)
+            out["dense_L163840"] = path_record(ms, bytes_dense(L), 1, ti)
+            if want_cpu:
+                us, reps = cpu_dense_b1(L)
+                out["dense_L163840"]["cpu_b1_us_per_step"] = round(us, 1)
+                out["dense_L163840"]["cpu_b32_us_per_step_extrapolated"] = round(us * B, 1)
+                out["dense_L163840"]["cpu_note"] = (f"measured on one sequence (B=1, {reps} reps); the B=32 "
+                                                    "figure is that x32, extrapolated, not measured")
+            progress(f"dense_L163840: {out['dense_L163840']['us_per_step']} us")
         if "paged" in paths:
             # the same cache scattered over 16-token pages ([pages, 16, KVH,
             # D], vLLM's layout) in a random order, every sequence at full
@@ -437,9 +547,9 @@ def main():
             vp = torch.empty_like(kp)
             vp[idx] = v.view(B, KVH, nb, ps, D).permute(0, 2, 3, 1, 4).reshape(-1, ps, KVH, D)
             lens = torch.full((B,), L, dtype=torch.int32, device=dev)
-            ms, _ = graph_time(lambda i: paged_kernel.paged_decode_attention(
-                q, kp, vp, table, lens, max_seq_len=L, kv_layout="NHD"), 1, dsteps, 1)
-            out["paged_nhd16_L163840"] = path_record(ms, bytes_paged(L, ps), 1, dsteps)
+            ms, ti = graph_time(lambda i: paged_kernel.paged_decode_attention(
+                q, kp, vp, table, lens, max_seq_len=L, kv_layout="NHD"), 1, Kms, ms_warm, replays=2)
+            out["paged_nhd16_L163840"] = path_record(ms, bytes_paged(L, ps), 1, ti)
             del kp, vp, table, idx, lens
         del k, v
         if "dense" in paths:
@@ -453,13 +563,63 @@ def main():
                 qq, kk, vv = dsets[i]
                 return dense_kernel.dense_decode_attention(qq, kk, vv, seq_len=Ls)
 
-            ms, _ = graph_time(dcall, ns, max(3, K // 2), 1)
-            out["dense_L32768"] = path_record(ms, bytes_dense(Ls), ns, max(3, K // 2))
+            ms, ti = graph_time(dcall, ns, Kms, ms_warm, replays=2)
+            out["dense_L32768"] = path_record(ms, bytes_dense(Ls), ns, ti)
             del dsets
+        torch.cuda.empty_cache()
+
+    grid = None
+    if "grid" in paths:
+        grid = {"note": "dense per L; sparse and fused KIVI per W at L=163840 (steady state: the same "
+                        "bytes at every L >= S + W); cpu_b1_us = the same step for one sequence "
+                        "(B=1) on the host, float32 torch restatement",
+                "dense": {}, "sparse": {}, "kivi": {}}
+        for Lg in CONTEXT_LENGTHS:
+            qq, kk, vv = randn(B, H, D), randn(B, KVH, Lg, D), randn(B, KVH, Lg, D)
+            ms, ti = graph_time(lambda i: dense_kernel.dense_decode_attention(qq, kk, vv, seq_len=Lg), 1,
+                                Kms, ms_warm, replays=2)
+            rec = path_record(ms, bytes_dense(Lg), 1, ti)
+            if want_cpu:
+                rec["cpu_b1_us"] = round(cpu_dense_b1(Lg)[0], 1)
+            grid["dense"][str(Lg)] = rec
+            del qq, kk, vv
+            torch.cuda.empty_cache()
+        progress("grid dense done")
+        for wg in WINDOW_SIZES:
+            ns = n_sets(bytes_sparse(wg))
+            sets = [(randn(B, H, D),) + compacted(wg) for _ in range(ns)]
+
+            def call(i, sets=sets, wg=wg):
+                q, kc, vc = sets[i]
+                return sparse_kernel.sparse_decode_attention(q, kc, vc, seq_len=L, window=wg)
+
+            ms, ti = graph_time(call, ns, K, Wu)
+            rec = path_record(ms, bytes_sparse(wg), ns, ti)
+            if want_cpu:
+                rec["cpu_b1_us"] = round(cpu_sparse(1, wg)[0], 1)
+            grid["sparse"][str(wg)] = rec
+            del sets
+        progress("grid sparse done")
+        for wg in [32] + [w for w in WINDOW_SIZES if w >= R]:
+            ns, sets = kivi_sets(wg)
+            ms, ti = graph_time(kivi_call(sets, wg), ns, K, Wu)
+            rec = path_record(ms, bytes_kivi(wg), ns, ti, bytes_kivi(wg, sink_tokens=32))
+            if want_cpu:
+                q0, parts = sets[0]
+                cache = {k_: t[:1] for k_, t in zip(KIVI_KEYS, parts)}
+                rec["cpu_b1_us"] = round(cpu_kivi(q0[:1], cache, wg, budget_s=1.0)[0], 1)
+            grid["kivi"][str(wg)] = rec
+            del sets
+            torch.cuda.empty_cache()
+        progress("grid kivi done")
+
+    if want_cpu:
+        cpu["config1_dense_L8192_b1"] = cpu_config1()
 
     head_key = "kivi_w256" if "kivi_w256" in out else next(iter(out))
     head = out[head_key]
     value = head["us_per_step"]
+    traffic, traffic_src = measured_traffic(head_key)
     line = {
         "metric": METRIC,
         "value": value,
@@ -475,12 +635,20 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{head_key}: B=32 H=64 KVH=8 D=128 L=163840 S=4 W=256 R=128, "
                                "fp16 N(0,1), 4 K channels x10",
-                   "timing": "HIP-graph replay of back-to-back steps over rotating cold input sets"},
+                   "timing": f"HIP graph of max(K, input sets) back-to-back steps over rotating cold "
+                             f"input sets, R back-to-back replays between two events, time / (R * "
+                             f"graph steps); this path: graph_steps={head['graph_steps']}, "
+                             f"replays={head['replays']}"},
         "roofline": {"bound": "hbm", "achieved": head["achieved_GBs"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": head["frac_of_peak"], "traffic": measured_traffic(head_key)},
-        "cpu_baseline": cpu,
+                     "unit": "GB/s", "frac": head["frac_of_peak"], "traffic": traffic,
+                     "traffic_source": traffic_src},
+        "cpu_baseline": head_cpu,
         "paths": out,
     }
+    if grid is not None:
+        line["grid"] = grid
+    if cpu is not None:
+        line["cpu"] = cpu
     print(json.dumps(line), flush=True)
 
 

@@ -391,12 +391,15 @@ __device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lan
 //                 tokens 0..31
 //   [2560, 2816)  V scales transposed [4 groups][32 tokens],
 //   [2816, 3072)  V zeros transposed
-constexpr int kQsK = 0, kQsKS = 1024, kQsKZ = 1280, kQsV = 1536, kQsVS = 2560, kQsVZ = 2816;
+//   [3072, 3328)  K zeros [128] as stored (the exact-zero path)
+constexpr int kQsK = 0, kQsKS = 1024, kQsKZ = 1280, kQsV = 1536, kQsVS = 2560, kQsVZ = 2816,
+              kQsKZr = 3072;
 
 __device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
   *reinterpret_cast<u32x4*>(slot + kQsK + 16 * lane) = X.kc;
   *reinterpret_cast<uint32_t*>(slot + kQsKS + 4 * lane) = X.ks;
   *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = pk_sub_f16(X.kz, 0xe400e400u);   // + 1024
+  *reinterpret_cast<uint32_t*>(slot + kQsKZr + 4 * lane) = X.kz;
   // lane L holds code bytes 16(L%2) .. +15 of token L/2
   const int tok = lane >> 1, b0 = 16 * (lane & 1);
 #pragma unroll
@@ -433,9 +436,16 @@ __device__ __forceinline__ uint32_t codes_1024(uint32_t c, uint32_t sel) {
 // PV.  Masked tokens get p = 0; their codes are finite.
 //   FOLD: every V zero of the tile has |zero| <= kFoldZeroMax, so
 //       (code - zero) * 4^k * 2^-8 is one exact fp16 (one MFMA pair per
-//       16 channels); otherwise code and zero go through separate MFMAs.
+//       16 channels), and every K zero has |zero| <= kFoldKZeroMax, so
+//       1024 + zero and code - zero are exact fp16 integers.  Otherwise
+//       codes and zeros go through separate MFMAs: V as below, K as the
+//       exact codes against q * scale plus one zero term per head,
+//       -sum_ch zero[ch] * q[ch] * scale[ch] (the same for every token),
+//       taken from the zeros as stored (fp16, exact) against the same
+//       head and remainder of q * scale.
 constexpr float kSlackVScale = 128.0f;
 constexpr float kFoldZeroMax = 1000.0f;
+constexpr float kFoldKZeroMax = 1024.0f;
 
 template <bool MIXED, bool HALF, bool FOLD>
 __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[4], int slot0,
@@ -459,20 +469,28 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   // dequantized K exactly instead of fp16 roundings of scale * (code - zero).
   const uint32_t sh = 2u * (uint32_t)(t & 3);
   float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  float4v sz = {0.f, 0.f, 0.f, 0.f};   // !FOLD: the zero term of every token row
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const half8 qh = qB[c] * ks[c];
     const half8 ql = __builtin_elementwise_fma(qB[c], ks[c], -qh);
+    if (!FOLD) {
+      const half8 nz = -*reinterpret_cast<const half8*>(slot + kQsKZr + 2 * (32 * c + 8 * g));
+      sz = mfma16x16x32(as_u4(nz), qh, sz);
+      sz = mfma16x16x32(as_u4(nz), ql, sz);
+    }
 #pragma unroll
     for (int blk = 0; blk < (HALF ? 1 : 2); ++blk) {
       const u32x2 w =
           *reinterpret_cast<const u32x2*>(slot + kQsK + (4 * blk + (t >> 2)) * 128 + 32 * c + 8 * g);
       const uint32_t c0 = (w[0] >> sh) & 0x03030303u;
       const uint32_t c1 = (w[1] >> sh) & 0x03030303u;
-      const u32x4 d = {pk_sub_f16(codes_1024(c0, 0x00050004u), kz1[c][0]),
-                       pk_sub_f16(codes_1024(c0, 0x00070006u), kz1[c][1]),
-                       pk_sub_f16(codes_1024(c1, 0x00050004u), kz1[c][2]),
-                       pk_sub_f16(codes_1024(c1, 0x00070006u), kz1[c][3])};
+      // FOLD: (1024 + code) - (1024 + zero); otherwise (1024 + code) - 1024
+      const u32x4 kz = FOLD ? kz1[c] : u32x4{0x64006400u, 0x64006400u, 0x64006400u, 0x64006400u};
+      const u32x4 d = {pk_sub_f16(codes_1024(c0, 0x00050004u), kz[0]),
+                       pk_sub_f16(codes_1024(c0, 0x00070006u), kz[1]),
+                       pk_sub_f16(codes_1024(c1, 0x00050004u), kz[2]),
+                       pk_sub_f16(codes_1024(c1, 0x00070006u), kz[3])};
       if (blk == 0) {
         s0 = mfma16x16x32(d, qh, s0);
         s0 = mfma16x16x32(d, ql, s0);
@@ -481,6 +499,10 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
         s1 = mfma16x16x32(d, ql, s1);
       }
     }
+  }
+  if (!FOLD) {
+    s0 += sz;
+    s1 += sz;
   }
 
   float x[8];
@@ -577,10 +599,12 @@ __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
   const half2v vs = __builtin_bit_cast(half2v, raw.vs);
   const float slack =
       __ballot(!(fmaxf((float)vs[0], (float)vs[1]) <= kSlackVScale)) ? 0.0f : kRescaleSlack;
-  // and two of its 128 V zeros
+  // and two of its 128 V zeros and two of its 128 K zeros
   const half2v vz = __builtin_bit_cast(half2v, raw.vz);
+  const half2v kz = __builtin_bit_cast(half2v, raw.kz);
   const bool fold =
-      !__ballot(!(fmaxf(fabsf((float)vz[0]), fabsf((float)vz[1])) <= kFoldZeroMax));
+      !__ballot(!(fmaxf(fabsf((float)vz[0]), fabsf((float)vz[1])) <= kFoldZeroMax &&
+                  fmaxf(fabsf((float)kz[0]), fabsf((float)kz[1])) <= kFoldKZeroMax));
   if (fold) {
     if (xlim <= kTile / 2)
       q_tile_body<MIXED, true, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);

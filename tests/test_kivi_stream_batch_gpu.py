@@ -88,7 +88,8 @@ def test_batch_equals_single_sequence_caches(W, device):
             np.testing.assert_array_equal(host(batch.t["k_ring"][b])[:, rows], host(one.t["k_ring"][0])[:, rows])
             np.testing.assert_array_equal(host(batch.t["v_ring"][b])[:, rows], host(one.t["v_ring"][0])[:, rows])
             for name in ("k_win_packed", "k_win_scale", "k_win_zero", "v_win_packed", "v_win_scale",
-                         "v_win_zero", "k_sink_packed", "v_sink_scale"):
+                         "v_win_zero", "k_sink_packed", "k_sink_scale", "k_sink_zero",
+                         "v_sink_packed", "v_sink_scale", "v_sink_zero"):
                 np.testing.assert_array_equal(host(batch.t[name][b]), host(one.t[name][0]), err_msg=name)
             # the same arithmetic; with a dynamic work queue (W=1024) the
             # summation order may differ, so allow one fp16 ulp
@@ -178,3 +179,30 @@ def test_step_attend_equals_append_then_attend(W, device):
     for name in ("appended", "ring", "plan", "arrive"):
         np.testing.assert_array_equal(host(getattr(one, name)), host(getattr(two, name)), err_msg=name)
     assert int(host(one.appended).min()) >= 32
+
+
+@pytest.mark.parametrize("G", [1, 4, 16])
+def test_step_attend_query_group_sizes(G, device):
+    """step_attend with G = H / KVH query heads per KV head other than 8
+    (one head, a partial MFMA column block, all 16 columns): after every
+    step (evictions included) the output matches the CPU oracle's stream
+    state to half an fp16 ulp."""
+    from kivi_stream import KiviStreamBatch
+    B, KVH, D, W = 3, 2, 128, 256
+    H = G * KVH
+    L0, steps = S + W + 9, 40
+    gen = torch.Generator(device=device).manual_seed(300 + G)
+    kf = torch.randn(B, KVH, L0 + steps, D, generator=gen, device=device, dtype=torch.float16)
+    vf = torch.randn(B, KVH, L0 + steps, D, generator=gen, device=device, dtype=torch.float16)
+    q = torch.randn(steps, B, H, D, generator=gen, device=device, dtype=torch.float16)
+    batch = KiviStreamBatch.from_prefill(kf[:, :, :L0], vf[:, :, :L0], W)
+    kh, vh = host(kf), host(vf)
+    say(f"stream step_attend G={G}")
+    for i in range(steps):
+        o = host(batch.step_attend(q[i], kf[:, :, L0 + i], vf[:, :, L0 + i]))
+        if i % 7 != 3 and i != R // 4 + 3:
+            continue
+        oc, wlen = O.stream_cache(kh, vh, L0, L0 + i + 1, W)
+        ref = O.quantized_attention(host(q[i]), wlen, oc, SCALE)
+        assert max_abs(o, ref) < ATTN_TOL, i
+        assert_nearly_rounded(o, ref)

@@ -65,9 +65,21 @@ def test_stream_matches_builder_after_evictions(W, device):
         rows = cache.residual_rows()
         np.testing.assert_array_equal(host(cache.t["k_ring"])[:, :, rows], host(ref["k_residual"]))
         np.testing.assert_array_equal(host(cache.t["v_ring"])[:, :, rows], host(ref["v_residual"]))
-        for name in ("k_sink_packed", "k_sink_scale", "k_sink_zero", "v_sink_packed"):
+        for name in ("k_sink_packed", "k_sink_scale", "k_sink_zero",
+                     "v_sink_packed", "v_sink_scale", "v_sink_zero"):
             np.testing.assert_array_equal(host(cache.t[name]), host(ref[name]), err_msg=name)
         assert max_abs(host(o), host(o_ref)) < 1e-3
+        # and the CPU oracle: its builder on the same compacted cache gives
+        # the GPU builder's tensors, and its stream_cache state (pinned by a
+        # token-by-token model in test_oracle.py) the same attention
+        oc = O.build_quantized_kv_cache(host(comp_k), host(comp_v))
+        for key in O.CACHE_KEYS:
+            np.testing.assert_array_equal(host(ref[key]), oc[key], err_msg=key)
+        sc, wlen = O.stream_cache(host(kf), host(vf), L0, L, W)
+        for key in O.CACHE_KEYS:
+            np.testing.assert_array_equal(sc[key], oc[key], err_msg=key)
+        o_orc = O.quantized_attention(host(q), wlen, sc, SCALE)
+        assert max_abs(host(o), o_orc) < ATTN_TOL
 
 
 def test_stream_between_evictions_vs_oracle(device):

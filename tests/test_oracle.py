@@ -495,3 +495,111 @@ def test_quantized_attention_composition_and_masking():
         ramp = O.quantized_attention_masked(q, cache, L, W, D**-0.5)
         valid = O.kv_indices(L, 0, W, S, S + W)[1]
         np.testing.assert_allclose(ramp, O.masked_attention(q, k, v, valid, D**-0.5), atol=0)
+
+
+# ----------------------------------------------------------------------------
+# decode-time (streaming) KIVI cache
+# ----------------------------------------------------------------------------
+
+def _stream_positions(prefill_len, n_appends, window, sink=4, residual=128, group=32):
+    """Token-by-token model of the streaming cache's attended positions: the
+    sink, the window-old groups (oldest first) and the fp16 residual.  Each
+    append joins the residual; when it holds residual + group tokens its
+    oldest `group` form a new window-old group and the oldest window-old
+    group leaves (with no window-old part the block leaves at once)."""
+    sinks = list(range(sink))
+    groups = [list(range(s, s + group))
+              for s in range(prefill_len - window, prefill_len - residual, group)]
+    res = list(range(prefill_len - residual, prefill_len))
+    for p in range(prefill_len, prefill_len + n_appends):
+        res.append(p)
+        if len(res) == residual + group:
+            block, res = res[:group], res[group:]
+            if groups:
+                groups = groups[1:] + [block]
+    return sinks, groups, res
+
+
+def _padded_sink(x, sink=4, group=32):
+    real = x[:, :, :sink]
+    return np.concatenate([real, np.repeat(real[:, :, :1], group - sink, axis=2)], axis=2)
+
+
+@pytest.mark.parametrize("W", [128, 160, 256])
+def test_stream_cache_follows_token_by_token_model(W):
+    """stream_cache after n = 0..200 appends holds exactly the positions the
+    token-by-token model attends, each regime quantized from those positions;
+    at every eviction point (n a multiple of 32) it is the reference
+    builder's output on the compacted cache [sink, L - W .. L)."""
+    S, R = 4, 128
+    L0 = S + W + 37
+    rng = _rng(500 + W)
+    kf = rng.standard_normal((1, 2, L0 + 201, 128)).astype(np.float16)
+    vf = rng.standard_normal((1, 2, L0 + 201, 128)).astype(np.float16)
+    sink_k = O.quantize_k(_padded_sink(kf).astype(F32))
+    sink_v = O.quantize_v(_padded_sink(vf).astype(F32))
+    for n in range(201):
+        L = L0 + n
+        cache, wlen = O.stream_cache(kf, vf, L0, L, W)
+        sinks, groups, res = _stream_positions(L0, n, W)
+        assert wlen == W - R == 32 * len(groups)
+        assert len(res) == R + n % 32 and res[-1] == L - 1
+        # every position attended exactly once, none twice
+        attended = sinks + sum(groups, []) + res
+        assert len(set(attended)) == len(attended) == S + W + n % 32
+        np.testing.assert_array_equal(cache["k_residual"], kf[:, :, res])
+        np.testing.assert_array_equal(cache["v_residual"], vf[:, :, res])
+        for name, (p, s, z) in (("k_sink", sink_k), ("v_sink", sink_v)):
+            np.testing.assert_array_equal(cache[name + "_packed"], p)
+            np.testing.assert_array_equal(cache[name + "_scale"], s)
+            np.testing.assert_array_equal(cache[name + "_zero"], z)
+        if groups:
+            pos = sum(groups, [])
+            for name, fn, src in (("k_win", O.quantize_k, kf), ("v_win", O.quantize_v, vf)):
+                p, s, z = fn(src[:, :, pos].astype(F32))
+                np.testing.assert_array_equal(cache[name + "_packed"], p)
+                np.testing.assert_array_equal(cache[name + "_scale"], s)
+                np.testing.assert_array_equal(cache[name + "_zero"], z)
+        if n % 32 == 0:
+            comp_k = np.concatenate([kf[:, :, :S], kf[:, :, L - W:L]], axis=2)
+            comp_v = np.concatenate([vf[:, :, :S], vf[:, :, L - W:L]], axis=2)
+            built = O.build_quantized_kv_cache(comp_k, comp_v)
+            for key in O.CACHE_KEYS:
+                np.testing.assert_array_equal(cache[key], built[key], err_msg=f"{key} n={n}")
+
+
+# ----------------------------------------------------------------------------
+# torch restatement used for the CPU baseline (oracle/torch_ref.py)
+# ----------------------------------------------------------------------------
+
+def test_torch_ref_matches_numpy_oracle():
+    """The torch CPU restatement that bench.py times as the CPU baseline
+    computes what the (independently pinned) numpy oracle computes: dense,
+    sink + window through ramp-up, unpack/dequant of both layouts, and the
+    quantized composition (float32 vs float64: 1e-5)."""
+    from oracle import torch_ref as T
+    rng = _rng(900)
+    t = torch.from_numpy
+    q = rng.standard_normal((2, 16, 128)).astype(F32)
+    k = rng.standard_normal((2, 2, 300, 128)).astype(F32)
+    v = rng.standard_normal((2, 2, 300, 128)).astype(F32)
+    sc = 128 ** -0.5
+    np.testing.assert_allclose(T.dense_attention(t(q), t(k), t(v), sc).numpy(),
+                               O.dense_attention(q, k, v, sc), atol=1e-5)
+    S, W = 4, 256
+    kc, vc = k[:, :, :S + W], v[:, :, :S + W]
+    for L in (1, 3, 4, 5, 100, 259, 260, 261, 5000):
+        want = O.sparse_attention_compacted(q, kc, vc, L, W, S, sc)
+        got = T.sparse_attention(t(q), t(kc), t(vc), L, W, S, sc).numpy()
+        np.testing.assert_allclose(got, want, atol=1e-5, err_msg=str(L))
+        np.testing.assert_array_equal(T.slot_validity(L, W, S, S + W).numpy(), O.slot_validity(L, W, S))
+    cache = O.build_quantized_kv_cache(kc.astype(np.float16), vc.astype(np.float16))
+    for name, n, axis in (("k_win", W - 128, 2), ("v_win", 128, 3)):
+        got = T.unpack_dequant(t(cache[name + "_packed"]), t(cache[name + "_scale"]), t(cache[name + "_zero"]),
+                               n, axis).numpy()
+        want = O.unpack_dequant(cache[name + "_packed"], cache[name + "_scale"], cache[name + "_zero"], n, axis)
+        np.testing.assert_array_equal(got, want)
+    tc = {key: t(np.ascontiguousarray(val)) for key, val in cache.items()}
+    q16 = q.astype(np.float16)
+    np.testing.assert_allclose(T.quantized_attention(t(q16), W - 128, tc, sc).numpy(),
+                               O.quantized_attention(q16, W - 128, cache, sc), atol=1e-5)

@@ -97,6 +97,28 @@ def test_quantized_attention_steady_state(W, device):
     assert max_abs(o, O.quantized_attention(qh, W - R, hc, SCALE, dtype=np.float32)) < REF_TOL
 
 
+@pytest.mark.parametrize("G", [1, 4, 16])
+@pytest.mark.parametrize("W", [256, 1024])
+def test_quantized_attention_query_group_sizes(G, W, device):
+    """G = H / KVH query heads per KV head other than 8: one head, a partial
+    MFMA column block, all 16 columns (the quantized tiles' publish writes
+    16 head rows in their own lane layout).  Static (W=256) and dynamic
+    (W=1024) work queues."""
+    from quant_kernel import build_quantized_kv_cache
+    B, KVH, D = 2, 4, 128
+    H = G * KVH
+    gen = torch.Generator(device=device).manual_seed(400 + G + W)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    say(f"kivi G={G} W={W}")
+    cache = build_quantized_kv_cache(kc, vc)
+    o = _attend(q, cache, 163840, W)
+    ref = O.quantized_attention(host(q), W - R, _host_cache(cache), SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
+    assert_nearly_rounded(o, ref)
+
+
 def test_quantized_attention_outlier_keys(device):
     """Config-5 distributions: K with 4 channels x10 (sharper softmax)."""
     from quant_kernel import build_quantized_kv_cache
@@ -160,6 +182,34 @@ def test_quantized_attention_large_v_offsets(device):
     assert np.abs(zeros).max() > 1000 and (np.abs(zeros) <= 3).any()
     o = _attend(q, cache, 163840, W)
     ref = O.quantized_attention(host(q), W - R, _host_cache(cache), SCALE)
+    assert_nearly_rounded(o, ref)
+
+
+@pytest.mark.parametrize("W", [256, 512])
+def test_quantized_attention_large_k_offsets(W, device):
+    """K channels far from zero relative to their spread (+-100, +-300 and
+    30 plus 0.05 N(0,1), in every token): K zero points of both signs up to
+    a few thousand (fp16 integers, even above 2048), in the sink and window
+    groups.  1024 + zero and code - zero are then not exact fp16, so those
+    tiles take the separate zero-term path; every output must stay within
+    half an fp16 ulp of the fp64 oracle (plus 5e-5)."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D = 2, 16, 2, 128
+    gen = torch.Generator(device=device).manual_seed(19 + W)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device)
+    for ch, off in [(3, 100.0), (17, -100.0), (40, 300.0), (77, -300.0), (90, 30.0)]:
+        kc[..., ch] = off + 0.05 * kc[..., ch]
+    kc = kc.half()
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    say(f"kivi large K offsets W={W}")
+    cache = build_quantized_kv_cache(kc, vc)
+    hc = _host_cache(cache)
+    zeros = np.concatenate([hc["k_win_zero"].ravel(), hc["k_sink_zero"].ravel()]).astype(np.float32)
+    assert zeros.max() > 2048 and zeros.min() < -2048
+    o = _attend(q, cache, 163840, W)
+    ref = O.quantized_attention(host(q), W - R, hc, SCALE)
+    assert max_abs(o, ref) < ATTN_TOL
     assert_nearly_rounded(o, ref)
 
 
