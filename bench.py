@@ -32,13 +32,15 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
 
 Timing.  Each path keeps enough independent input sets resident in HBM that
 one pass over them is >= 1 GiB (more than L2 plus the 256 MB Infinity
-Cache), captures G = max(K, sets) back-to-back calls cycling through every
-set in one HIP graph, replays it untimed, then times R back-to-back replays
-(R * G >= 1000 steps for the microsecond-scale paths, R = 2 for the
-millisecond-scale ones) between two HIP events on the capture stream:
-``us_per_step`` = that time / (R * G), the steady-state cost of a decode
-step whose inputs are cold in every cache, with launches pipelined as in a
-decode loop and the graphs' submission costs spread over all R * G steps.
+Cache), captures G back-to-back calls cycling through every set in one HIP
+graph, replays it untimed, then times R back-to-back replays between two
+HIP events on the capture stream: ``us_per_step`` = that time / (R * G), the
+steady-state cost of a decode step whose inputs are cold in every cache,
+with launches pipelined as in a decode loop.  A replay carries a fixed cost
+of its own (~20 us measured: a 51-step graph replayed 20 times gave 6.93 us
+per KIVI step where a 400-step graph gave 6.49), so the microsecond-scale
+paths use G = max(K, sets, 512) and R * G >= 1000 whatever K is; the
+millisecond-scale paths use G = min(K, 20) (at least 4) and R = 2.
 ``latency_us`` is the reference harness's method (triton do_bench): a 1 GiB
 buffer write before each single call, events around the call; it adds the
 per-call dispatch latency (about 5 us on this system for an empty kernel).
@@ -82,6 +84,7 @@ METRIC = "decode-attn µs/step + achieved HBM TB/s (% of peak), B=32 L=163840 W=
 COLD_SET_BYTES = 1 << 30           # one pass over a path's input sets reads at least this
 MAX_SETS = 512
 MIN_TIMED_STEPS = 1000             # microsecond-scale paths: R * G >= this
+MIN_GRAPH_STEPS = 512              # and G >= this: each replay costs ~20 us of its own
 CONTEXT_LENGTHS = [8192, 16384, 32768, 65536, 131072, 163840]          # constants.py:18
 WINDOW_SIZES = [0, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384]
 KERNEL_SOURCES = ("attn.hip", "kvdec_device.h", "kvdec_stream.h", "quant.hip")
@@ -146,12 +149,16 @@ def bytes_quantize(n_tok):
 # timing
 # --------------------------------------------------------------------------
 
-def graph_time(call, nsets, steps, warmup, min_steps=MIN_TIMED_STEPS, replays=None):
-    """Per-step ms of back-to-back calls call(i % nsets), G = max(steps, nsets)
-    of them captured in one HIP graph (every input set once per pass), timed
-    over R back-to-back replays (R * G >= min_steps unless `replays` is
-    given).  Returns (ms_per_step, {"graph_steps": G, "replays": R})."""
-    G = max(steps, nsets)
+def graph_time(call, nsets, steps, warmup, min_steps=MIN_TIMED_STEPS, replays=None,
+               min_graph=MIN_GRAPH_STEPS):
+    """Per-step ms of back-to-back calls call(i % nsets), G = max(steps, nsets,
+    min_graph) of them captured in one HIP graph (every input set once per
+    pass), timed over R back-to-back replays (R * G >= min_steps unless
+    `replays` is given).  A replay carries a fixed cost (~20 us measured
+    between two back-to-back replays of one graph) that R * G steps share,
+    so G is kept long whatever `steps` is.  Returns (ms_per_step,
+    {"graph_steps": G, "replays": R})."""
+    G = max(steps, nsets, min_graph)
     Rp = replays if replays is not None else max(2, math.ceil(min_steps / G))
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -225,7 +232,7 @@ def measured_traffic(key):
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs recorded in profiles/
     hbm_traffic.json; bytes are None when nothing is recorded or the record
     was measured on other kernel sources."""
-    src = {"file": "profiles/hbm_traffic.json", "key": key}
+    src = {"file": "profiles/hbm_traffic.json", "key": key, "current_source_sha16": kernel_source_hash()}
     try:
         with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
             rec = json.load(f).get(key)
@@ -233,8 +240,7 @@ def measured_traffic(key):
         rec = None
     if rec is None:
         return None, {**src, "status": "not recorded"}
-    src.update(commit=rec.get("commit"), recorded_source_sha16=rec.get("source_sha16"),
-               current_source_sha16=kernel_source_hash())
+    src.update(commit=rec.get("commit"), recorded_source_sha16=rec.get("source_sha16"))
     if rec.get("source_sha16") != src["current_source_sha16"]:
         return None, {**src, "status": "stale: recorded on other kernel sources"}
     return int(rec["fetch_bytes_per_launch"] + rec["write_bytes_per_launch"]), {**src, "status": "current"}
@@ -516,14 +522,14 @@ def main():
         v = randn(B, KVH, L, D)
         q = randn(B, H, D)
         if "quantize" in paths:
-            ms, ti = graph_time(lambda i: quant_kernel.quantize_k_cache(k), 1, Kms, ms_warm, replays=2)
+            ms, ti = graph_time(lambda i: quant_kernel.quantize_k_cache(k), 1, Kms, ms_warm, replays=2, min_graph=1)
             out["quantize_k_L163840"] = path_record(ms, bytes_quantize(L), 1, ti)
-            ms, ti = graph_time(lambda i: quant_kernel.quantize_v_cache(v), 1, Kms, ms_warm, replays=2)
+            ms, ti = graph_time(lambda i: quant_kernel.quantize_v_cache(v), 1, Kms, ms_warm, replays=2, min_graph=1)
             out["quantize_v_L163840"] = path_record(ms, bytes_quantize(L), 1, ti)
             progress("quantize done")
         if "dense" in paths:
             ms, ti = graph_time(lambda i: dense_kernel.dense_decode_attention(q, k, v, seq_len=L), 1,
-                                Kms, ms_warm, replays=2)
+                                Kms, ms_warm, replays=2, min_graph=1)
             out["dense_L163840"] = path_record(ms, bytes_dense(L), 1, ti)
             if want_cpu:
                 us, reps = cpu_dense_b1(L)
@@ -548,7 +554,7 @@ def main():
             vp[idx] = v.view(B, KVH, nb, ps, D).permute(0, 2, 3, 1, 4).reshape(-1, ps, KVH, D)
             lens = torch.full((B,), L, dtype=torch.int32, device=dev)
             ms, ti = graph_time(lambda i: paged_kernel.paged_decode_attention(
-                q, kp, vp, table, lens, max_seq_len=L, kv_layout="NHD"), 1, Kms, ms_warm, replays=2)
+                q, kp, vp, table, lens, max_seq_len=L, kv_layout="NHD"), 1, Kms, ms_warm, replays=2, min_graph=1)
             out["paged_nhd16_L163840"] = path_record(ms, bytes_paged(L, ps), 1, ti)
             del kp, vp, table, idx, lens
         del k, v
@@ -563,7 +569,7 @@ def main():
                 qq, kk, vv = dsets[i]
                 return dense_kernel.dense_decode_attention(qq, kk, vv, seq_len=Ls)
 
-            ms, ti = graph_time(dcall, ns, Kms, ms_warm, replays=2)
+            ms, ti = graph_time(dcall, ns, Kms, ms_warm, replays=2, min_graph=1)
             out["dense_L32768"] = path_record(ms, bytes_dense(Ls), ns, ti)
             del dsets
         torch.cuda.empty_cache()
@@ -577,7 +583,7 @@ def main():
         for Lg in CONTEXT_LENGTHS:
             qq, kk, vv = randn(B, H, D), randn(B, KVH, Lg, D), randn(B, KVH, Lg, D)
             ms, ti = graph_time(lambda i: dense_kernel.dense_decode_attention(qq, kk, vv, seq_len=Lg), 1,
-                                Kms, ms_warm, replays=2)
+                                Kms, ms_warm, replays=2, min_graph=1)
             rec = path_record(ms, bytes_dense(Lg), 1, ti)
             if want_cpu:
                 rec["cpu_b1_us"] = round(cpu_dense_b1(Lg)[0], 1)
