@@ -88,6 +88,22 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o,
                        void* stream);
 
 /*
+ * kvdec_dense_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The split-K partials go to a file-scope device array of
+ * 4160 KiB that each GPU holds until the process ends (every shape the
+ * split plan allows fits; a larger need returns KVDEC_E_WORKSPACE).  The
+ * call allocates nothing.  All calls on one GPU share that array: calls
+ * that overlap on one GPU (two streams) race.  Nothing in it needs to
+ * start at zero (each call writes every partial it reads).  `stream` must
+ * belong to the current device.  Results are those of kvdec_dense_decode.
+ */
+int kvdec_dense_decode_noalloc(const void* q, const void* k, const void* v, void* o,
+                               int dtype, int64_t B, int32_t H, int32_t KVH,
+                               int64_t L, int32_t D, float sm_scale, void* stream);
+
+/*
  * StreamingLLM sink + window decode over a compacted [B, KVH, sink+window, D]
  * fp16 cache.  Replaces sparse_kernel.py:105-118 (sparse_decode_attention) and
  * sparse_kernel.py:67-102; slot validity follows _kv_indices

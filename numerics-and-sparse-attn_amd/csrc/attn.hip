@@ -24,7 +24,18 @@
 #include "kvdec_stream.h"
 #include "kvdec.h"
 
+#include <mutex>
+
 using namespace kvdec;
+
+// Workspace of kvdec_dense_decode_noalloc: the split-K partials of one call
+// (fp32 [units][G][128] outputs, then [units][G] maxima and sums), in a
+// file-scope device array that every GPU the library runs on holds until
+// the process ends.  The launch plan splits only while there are fewer than
+// 256 work units, so one call has at most 2 * 255 units of at most 16 heads:
+// 510 * 16 * 130 * 4 = 4,243,200 bytes.
+constexpr size_t kScratchBytes = (size_t)4160 << 10;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
 
@@ -909,6 +920,40 @@ int launch_attn(AttnCommon P, const Src& S, bool kivi, size_t ws_bytes, hipStrea
 
 // The fused KIVI decode at one length (lens null) or at per-sequence
 // lengths lens[b] (seq_len unused).
+// Device address of `scratch` on the current device, looked up once per
+// device (in host code the array's name is only a stand-in for the symbol).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return KVDEC_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return KVDEC_E_WORKSPACE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KVDEC_OK;
+}
+
+int check_dense(const void* q, const void* k, const void* v, void* o, int dtype, int64_t B,
+                int32_t H, int32_t KVH, int64_t L, int32_t D) {
+  if (!q || !k || !v || !o) return KVDEC_E_NULL;
+  if (dtype != KVDEC_F16) return KVDEC_E_DTYPE;
+  int rc = check_heads(B, H, KVH, D);
+  if (rc) return rc;
+  if (L < 1) return KVDEC_E_SEQLEN;
+  if (L * kRowBytes >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;   // 32-bit in-head offsets
+  return KVDEC_OK;
+}
+
 int kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
                 void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH, int64_t seq_len,
                 int32_t window, int32_t sink, int32_t residual, int32_t group, int32_t bits,
@@ -1159,12 +1204,8 @@ size_t kvdec_workspace_bytes(int kind, int64_t B, int32_t H, int32_t KVH, int64_
 int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int dtype, int64_t B,
                        int32_t H, int32_t KVH, int64_t L, int32_t D, float sm_scale, void* ws,
                        size_t ws_bytes, void* stream) {
-  if (!q || !k || !v || !o) return KVDEC_E_NULL;
-  if (dtype != KVDEC_F16) return KVDEC_E_DTYPE;
-  int rc = check_heads(B, H, KVH, D);
+  int rc = check_dense(q, k, v, o, dtype, B, H, KVH, L, D);
   if (rc) return rc;
-  if (L < 1) return KVDEC_E_SEQLEN;
-  if (L * kRowBytes >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;   // 32-bit in-head offsets
   AttnCommon P{};
   P.q = static_cast<const _Float16*>(q);
   P.o = static_cast<_Float16*>(o);
@@ -1178,6 +1219,21 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int
   P.R = SlotRanges{(int)L, 0, 0};
   F16Src S{static_cast<const _Float16*>(k), static_cast<const _Float16*>(v), (int)L};
   return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int kvdec_dense_decode_noalloc(const void* q, const void* k, const void* v, void* o, int dtype,
+                               int64_t B, int32_t H, int32_t KVH, int64_t L, int32_t D,
+                               float sm_scale, void* stream) {
+  int rc = check_dense(q, k, v, o, dtype, B, H, KVH, L, D);
+  if (rc) return rc;
+  const size_t need = kvdec_workspace_bytes(KVDEC_KIND_DENSE, B, H, KVH, L, D);
+  if (need > kScratchBytes) return KVDEC_E_WORKSPACE;
+  void* ws = nullptr;
+  if (need > 0) {
+    rc = scratch_address(&ws);
+    if (rc) return rc;
+  }
+  return kvdec_dense_decode(q, k, v, o, dtype, B, H, KVH, L, D, sm_scale, ws, need, stream);
 }
 
 int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache, void* o,

@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 20
+    assert len(funcs) == 21
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -107,6 +107,22 @@ def test_dense_validation():
     # calls must fail validation: FAKE pointers are never launched on)
     assert _dense(B=1, L=163840) == E["WORKSPACE"]
     assert _dense(B=1, L=163840, ws=FAKE, wsb=16) == E["WORKSPACE"]
+
+
+def test_dense_noalloc_validation():
+    """The workspace-free dense decode rejects bad arguments before it looks
+    up its device array or launches anything."""
+    def call(**kw):
+        a = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, dtype=K.F16, B=32, H=64, KVH=8, L=5000, D=128)
+        a.update(kw)
+        return K.lib.kvdec_dense_decode_noalloc(a["q"], a["k"], a["v"], a["o"], a["dtype"], a["B"], a["H"],
+                                                a["KVH"], a["L"], a["D"], 0.088, None)
+    assert call(q=None) == E["NULL"]
+    assert call(dtype=K.F32) == E["DTYPE"]
+    assert call(KVH=7) == E["SHAPE"]
+    assert call(D=64) == E["SHAPE"]
+    assert call(L=0) == E["SEQLEN"]
+    assert call(L=1 << 23) == E["SHAPE"]
 
 
 def _sparse(**kw):
