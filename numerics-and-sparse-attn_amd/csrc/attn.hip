@@ -124,8 +124,8 @@ template <bool MIXED>
 struct QItems {
   typedef QTileRaw Raw;
   typedef QRef State;
-  QRegion sinkq, winq;
-  int n, sink;   // n = nwt + 1
+  QRegion sinkq, winq;   // this KV head's sink group and window-old groups
+  int n, sink;           // n = nwt + 1
   __device__ __forceinline__ void load(int i, Raw& X, int lane) const {
     const bool s = i == n - 1;
     QRegion Q;
@@ -223,23 +223,25 @@ __device__ __forceinline__ void publish_f(const AttnCommon& P, const WaveState& 
   }
 }
 
-// Quantized-tile accumulators: lane (t, g) holds head 4g + r, channel
-// 16 blk + t, scaled by 1 / q_state_scale().  All 16 head rows are written
-// (rows of heads >= G stay inside the wave's slot and the merge never reads
-// them), so no write is predicated.  ADD: the slot already holds this wave's
-// fp16-tile rows (all reads are issued before any write, so the adds wait on
-// LDS once).
+// Quantized-tile accumulators: lane (t, g) holds head 4g + r of channel
+// q_state_channel(grp, m, t) in QState::O[2 grp + m], scaled by
+// 1 / q_state_scale().  All 16 head rows are written (rows of heads >= G
+// stay inside the wave's slot and the merge never reads them), so no write
+// is predicated.  ADD: the slot already holds this wave's fp16-tile rows
+// (all reads are issued before any write, so the adds wait on LDS once).
 template <bool ADD>
 __device__ __forceinline__ void publish_q(QState& qs, char* slot, int lane) {
   const int t = lane & 15, g = lane >> 4;
-  const float f = q_state_scale(lane);
+  const float f = q_state_scale();
 #pragma unroll
   for (int blk = 0; blk < 8; ++blk) qs.O[blk] = qs.O[blk] * f;
   uint32_t off[8][4];
 #pragma unroll
-  for (int blk = 0; blk < 8; ++blk)
+  for (int blk = 0; blk < 8; ++blk) {
+    const int ch = q_state_channel(blk >> 1, blk & 1, t);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) off[blk][r] = row_off(4 * g + r, 4 * blk + (t >> 2)) + 4 * (t & 3);
+    for (int r = 0; r < 4; ++r) off[blk][r] = row_off(4 * g + r, ch >> 2) + 4 * (ch & 3);
+  }
   if (ADD) {
     float prev[8][4];
 #pragma unroll

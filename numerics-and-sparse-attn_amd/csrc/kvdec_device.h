@@ -352,13 +352,13 @@ __device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, bool valid,
 // share).  The PV product of a quantized tile is computed transposed,
 // O[head][channel] = P'[head][token] . (code - zero)[token][channel], with
 // each MFMA covering 16 channels of one 32-channel V quantization group, so
-// the per-token V scale folds into P' = p * scale.  The B operand is the
-// code as it sits in its byte (code * 4^k, k = t % 4, the channel's position
-// in the byte) minus zero * 4^k, times 2^-8: exact normal fp16 values (the
-// MFMA rounds products of fp16 subnormals to about 2^-13, so the operand is
-// kept out of the subnormal range).
-//   O[blk][r] : 4^k 2^-8 sum_t P'[t][head 4g + r] * (code - zero)[t][channel
-//               16 blk + t] for lane (t, g); q_state_scale() is 2^8 / 4^k
+// the per-token V scale folds into P' = p * scale.  The B operand is
+// (code - zero) * 2^-8: exact normal fp16 values (the MFMA rounds products
+// of fp16 subnormals to about 2^-13, so the operand is kept out of the
+// subnormal range).
+//   O[2 grp + m][r] : 2^-8 sum_t P'[t][head 4g + r] * (code - zero)[t][ch]
+//                     for lane (t, g), channel ch = 32 grp + 4 (t & 7) +
+//                     2 m + (t >> 3); q_state_scale() is 2^8
 struct QState {
   float4v O[8];
 };
@@ -368,9 +368,12 @@ __device__ __forceinline__ void q_state_init(QState& qs) {
   for (int b = 0; b < 8; ++b) qs.O[b] = float4v{0.f, 0.f, 0.f, 0.f};
 }
 
-// Factor that turns the lane's accumulators into output values.
-__device__ __forceinline__ float q_state_scale(int lane) {
-  return __builtin_ldexpf(1.0f, 8 - 2 * (lane & 3));
+// Factor that turns the accumulators into output values.
+__device__ __forceinline__ float q_state_scale() { return 256.0f; }
+
+// Output channel of accumulator column t of QState::O[2 grp + m].
+__device__ __forceinline__ int q_state_channel(int grp, int m, int t) {
+  return 32 * grp + 4 * (t & 7) + 2 * m + (t >> 3);
 }
 
 // Rescale by alpha, given per head in lane layout (head = lane & 15); the
@@ -387,8 +390,8 @@ __device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lan
 // Layout of a staged KIVI tile inside a wave slot (bytes):
 //   [0, 1024)     K codes, 8 byte rows x 128 channels (as stored)
 //   [1024, 1280)  K scales [128], [1280, 1536) 1024 + K zeros [128]
-//   [1536, 2560)  V codes transposed: row b (0..31) holds code byte b of
-//                 tokens 0..31
+//   [1536, 2560)  V codes, 32 token rows x 32 bytes (as stored; read back
+//                 transposed by ds_read_b64_tr_b8)
 //   [2560, 2816)  V scales transposed [4 groups][32 tokens],
 //   [2816, 3072)  V zeros transposed
 //   [3072, 3328)  K zeros [128] as stored (the exact-zero path)
@@ -400,18 +403,33 @@ __device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int l
   *reinterpret_cast<uint32_t*>(slot + kQsKS + 4 * lane) = X.ks;
   *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = pk_sub_f16(X.kz, 0xe400e400u);   // + 1024
   *reinterpret_cast<uint32_t*>(slot + kQsKZr + 4 * lane) = X.kz;
-  // lane L holds code bytes 16(L%2) .. +15 of token L/2
-  const int tok = lane >> 1, b0 = 16 * (lane & 1);
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    *reinterpret_cast<uint8_t*>(slot + kQsV + (b0 + i) * 32 + tok) =
-        (uint8_t)(X.vc[i >> 2] >> (8 * (i & 3)));
+  *reinterpret_cast<u32x4*>(slot + kQsV + 16 * lane) = X.vc;
   // lane L holds the scale / zero of token L/2, groups 2(L%2) and 2(L%2)+1
-  const int g0 = 2 * (lane & 1);
+  const int tok = lane >> 1, g0 = 2 * (lane & 1);
   *reinterpret_cast<uint16_t*>(slot + kQsVS + g0 * 64 + 2 * tok) = (uint16_t)X.vs;
   *reinterpret_cast<uint16_t*>(slot + kQsVS + (g0 + 1) * 64 + 2 * tok) = (uint16_t)(X.vs >> 16);
   *reinterpret_cast<uint16_t*>(slot + kQsVZ + g0 * 64 + 2 * tok) = (uint16_t)X.vz;
   *reinterpret_cast<uint16_t*>(slot + kQsVZ + (g0 + 1) * 64 + 2 * tok) = (uint16_t)(X.vz >> 16);
+}
+
+// Transposed LDS read (gfx950 ds_read_b64_tr_b8).  In each group of 16
+// lanes, lane 2j + h supplies the address of row j (8 bytes; h picks
+// columns 8h .. 8h + 7 of a 16-byte row) and lane i receives byte i of every
+// row: result byte j = row j, column i.
+__device__ __forceinline__ u32x2 lds_read_tr8(const char* p) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(p));
+  return u32x2{(uint32_t)r[0], (uint32_t)r[1]};
+}
+
+// fp16(a0 * b.lo - c.lo) in the low half and fp16(a1 * b.hi - c.hi) in the
+// high half of the result, from the fp32 a0, a1 and the fp16 pairs b, c:
+// v_fma_mixlo_f16 then v_fma_mixhi_f16 (each writes its half of the dword).
+__device__ __forceinline__ uint32_t fma_mix_pk_f16(float a0, float a1, uint32_t b, uint32_t c) {
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,1,1]" : "=v"(d) : "v"(a0), "v"(b), "v"(c));
+  asm("v_fma_mixhi_f16 %0, %1, %2, -%3 op_sel:[0,1,1] op_sel_hi:[0,1,1]" : "+v"(d) : "v"(a1), "v"(b), "v"(c));
+  return d;
 }
 
 // Two codes of `c` (one code per byte; sel 0x00050004 takes bytes 0 and 1,
@@ -538,52 +556,55 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   }
   st.l += ls;
 
-  // P' = p * scale per V group as an fp16 head pq + fp16 remainder pl (as
-  // for fp16 tiles).  tau(g, 0..3) = 4g..4g+3 and tau(g, 4..7) =
-  // 16 + 4g .. +3 sit contiguously in the transposed rows.
-  const _Float16 k4 = (_Float16)__builtin_ldexpf(1.0f, 2 * (t & 3) - 8);   // 4^k 2^-8
-  const uint32_t vmask = 0x03030303u << sh;
-  // PV, one V group (two 16-channel blocks) at a time: lane (t, g) feeds
-  // channel 16 blk + t of the tokens tau(g, j) (transposed code byte row
-  // 4 blk + t/4, bits 2k, 2k + 1 with k = t % 4).  The masked byte in the
-  // low byte of 0x64xx is the fp16 1024 + code * 4^k; times 2^-8 that is
-  // 4 + code * 4^k * 2^-8, so one fused multiply-add against
-  // 4 + zero * 4^k * 2^-8 (FOLD) or 4 leaves the exact operand.  Each
-  // product is taken with the head and the remainder of P'.
+  // PV, one V group (32 channels, code byte columns 8 grp .. 8 grp + 7) at
+  // a time.  One transposed LDS read gives lane (t, g) byte column
+  // 8 grp + (t & 7) of the tokens tau(g, 0..7) (lane t of each lane group
+  // supplies the row of token tau(g, t / 2)); MFMA m takes field
+  // f = 2 m + (t >> 3) of those bytes (channel 32 grp + 4 (t & 7) + f),
+  // shifted down to bits 0..1.  The masked byte in the low byte of 0x64xx
+  // is the fp16 1024 + code; times 2^-8 that is 4 + code * 2^-8, so one
+  // fused multiply-add against 4 + zero * 2^-8 (FOLD) or 4 leaves
+  // (code - zero) * 2^-8 or code * 2^-8, exactly.  P' = p * scale (the
+  // per-token V scale of the group) is taken as an fp16 head pq and the
+  // fp16 remainder pl (as for fp16 tiles); tau(g, 0..3) = 4g..4g+3 and
+  // tau(g, 4..7) = 16 + 4g .. +3 sit contiguously in the transposed
+  // scale and zero rows.
+  const char* vrow = slot + kQsV + 32 * tau(g, t >> 1);
+  const uint32_t vsh[2] = {2u * (uint32_t)(t >> 3), 2u * (uint32_t)(t >> 3) + 4u};
+  const half8 r8 = {0.00390625f, 0.00390625f, 0.00390625f, 0.00390625f,
+                    0.00390625f, 0.00390625f, 0.00390625f, 0.00390625f};   // 2^-8
+  const half8 four = {4, 4, 4, 4, 4, 4, 4, 4};
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
     const u32x2 s_lo = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 8 * g);
     const u32x2 s_hi = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 32 + 8 * g);
     const u32x2 z_lo = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 8 * g);
     const u32x2 z_hi = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 32 + 8 * g);
-    const half8 vsc = as_h8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
-    // head: fp16 product of the fp16 p and scale; remainder: the exact
-    // p * scale - head, rounded once (one fused multiply-add)
-    const half8 pq = pB * vsc;
-    half8 pl;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) pl[j] = (_Float16)__builtin_fmaf(pf[j], (float)vsc[j], -(float)pq[j]);
+    const u32x2 vb = lds_read_tr8(vrow + 8 * grp);
+    const u32x4 vsc = {s_lo[0], s_lo[1], s_hi[0], s_hi[1]};
+    // head: fp16 product of the fp16 p and scale; remainder: p * scale -
+    // head, rounded once (one mixed-precision fused multiply-add per value)
+    const u32x4 pq = as_u4(pB * as_h8(vsc));
+    const u32x4 pl = {fma_mix_pk_f16(pf[0], pf[1], vsc[0], pq[0]), fma_mix_pk_f16(pf[2], pf[3], vsc[1], pq[1]),
+                      fma_mix_pk_f16(pf[4], pf[5], vsc[2], pq[2]), fma_mix_pk_f16(pf[6], pf[7], vsc[3], pq[3])};
     const half8 zv = as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]});
-    const half8 four = {4, 4, 4, 4, 4, 4, 4, 4};
-    // FOLD: 4 + zero * 4^k 2^-8 (exact for |zero| <= kFoldZeroMax);
-    // otherwise -zero * 4^k 2^-8 for the separate zero term (exact)
-    const half8 zt = FOLD ? __builtin_elementwise_fma(zv, half8(k4), four) : zv * half8(-k4);
+    // FOLD: 4 + zero * 2^-8 (exact for |zero| <= kFoldZeroMax); otherwise
+    // -zero * 2^-8 for the separate zero term (exact)
+    const half8 zt = FOLD ? __builtin_elementwise_fma(zv, r8, four) : zv * -r8;
     const half8 off = FOLD ? zt : four;
 #pragma unroll
-    for (int blk = 2 * grp; blk < 2 * grp + 2; ++blk) {
-      const char* row = slot + kQsV + (4 * blk + (t >> 2)) * 32;
-      const uint32_t c0 = *reinterpret_cast<const uint32_t*>(row + 4 * g) & vmask;
-      const uint32_t c1 = HALF ? 0u : *reinterpret_cast<const uint32_t*>(row + 16 + 4 * g) & vmask;
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t c0 = (vb[0] >> vsh[m]) & 0x03030303u;
+      const uint32_t c1 = HALF ? 0u : (vb[1] >> vsh[m]) & 0x03030303u;
       const u32x4 bc = {codes_1024(c0, 0x00050004u), codes_1024(c0, 0x00070006u),
                         codes_1024(c1, 0x00050004u), codes_1024(c1, 0x00070006u)};
-      const half8 r8 = {0.00390625f, 0.00390625f, 0.00390625f, 0.00390625f,
-                        0.00390625f, 0.00390625f, 0.00390625f, 0.00390625f};   // 2^-8
       const half8 b = __builtin_elementwise_fma(as_h8(bc), r8, -off);
-      qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq, b, qs.O[blk], 0, 0, 0);
-      qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b, qs.O[blk], 0, 0, 0);
+      float4v& acc = qs.O[2 * grp + m];
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pq), b, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), b, acc, 0, 0, 0);
       if (!FOLD) {
-        qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pq, zt, qs.O[blk], 0, 0, 0);
-        qs.O[blk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, zt, qs.O[blk], 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pq), zt, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), zt, acc, 0, 0, 0);
       }
     }
   }
