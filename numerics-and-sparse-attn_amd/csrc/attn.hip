@@ -821,6 +821,220 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) 
   merge_out(P, lds, pair, split);
 }
 
+// ---------------------------------------------------------------------------
+// Lean single-pass kernels.  When a problem needs no split and every wave's
+// share is at most two tiles, one workgroup of 8 waves per KV head runs a
+// fixed program per wave: the KV head is the workgroup index (no division:
+// query row b * H + kvh * G of the head is head * G), every per-head address
+// is one multiply by a host-computed stride, and each wave issues its Q
+// operand and all of its tile loads before it waits on anything (no work
+// queue, no barrier before the merge).  The tile steps, the published
+// partials and the LDS merge are those of attn_kernel.
+// ---------------------------------------------------------------------------
+
+struct LeanCommon {
+  const _Float16* q;     // [heads][G][128]
+  _Float16* o;
+  float scale_log2;
+  int G;
+  SlotRanges R;
+};
+
+// The first part of every lean kernel: kernel-argument lines fetched in one
+// scalar-cache round trip, then the Q operand of this KV head's G query
+// heads in MFMA B-operand order (heads >= G read zeros without an access).
+template <class Args>
+__device__ __forceinline__ void lean_prologue(const LeanCommon& C, uint32_t head, int lane, half8 (&qB)[4]) {
+  {
+    constexpr int kArgLines = (int)(sizeof(Args) + 63) / 64;
+    static_assert(kArgLines <= 4, "kernel arguments span more lines than are touched");
+    const cint32* ka = (const cint32*)__builtin_amdgcn_kernarg_segment_ptr();
+    int32_t x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
+    asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]));
+  }
+  const int n = lane & 15, g = lane >> 4;
+  const rsrc_t rq = make_rsrc(C.q + (size_t)head * C.G * kHeadDim, (uint32_t)C.G * kRowBytes);
+  const uint32_t qoff = n < C.G ? (uint32_t)n * kRowBytes + 16u * (uint32_t)g : kOOB;
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc)
+    qB[cc] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 64u * cc, 0, 0));
+}
+
+// Barrier, then one thread per (head, 4 channels) combines the 8 waves'
+// published partials into the fp16 output rows of this KV head.
+__device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds, uint32_t head) {
+  __syncthreads();
+  const float* sh_m = reinterpret_cast<const float*>(lds + kLdsM);
+  const float* sh_l = reinterpret_cast<const float*>(lds + kLdsL);
+  const int e = threadIdx.x;
+  if (e >= C.G * 32) return;
+  const int hn = e >> 5, ch = e & 31;
+  float mw[kWaves], lw[kWaves];
+  float4v ow[kWaves];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    mw[w] = sh_m[w * kMaxGroup + hn];
+    lw[w] = sh_l[w * kMaxGroup + hn];
+    ow[w] = *reinterpret_cast<const float4v*>(lds + kLdsSlots + w * kSlotBytes + row_off(hn, ch));
+  }
+  float M = mw[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, mw[w]);
+  float L = 0.f;
+  float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float f = __builtin_amdgcn_exp2f(mw[w] - M);
+    L += lw[w] * f;
+    acc += ow[w] * f;
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
+              (_Float16)(acc[3] * inv)};
+  *reinterpret_cast<half4v*>(C.o + ((size_t)head * C.G + hn) * kHeadDim + 4 * ch) = h;
+}
+
+__device__ __forceinline__ void lean_publish_ml(int G, WaveState& st, char* lds, int lane, int wave) {
+  st.l = group_sum(st.l);
+  const int n = lane & 15, g = lane >> 4;
+  if (n < G && g == 0) {
+    reinterpret_cast<float*>(lds + kLdsM)[wave * kMaxGroup + n] = st.m;
+    reinterpret_cast<float*>(lds + kLdsL)[wave * kMaxGroup + n] = st.l;
+  }
+}
+
+__device__ __forceinline__ void lean_publish_f(int G, const WaveState& st, char* slot, int lane) {
+  AttnCommon P{};
+  P.G = G;
+  publish_f(P, st, slot, lane);
+}
+
+// fp16 rows [heads][rows][128] (the compacted sink + window cache, or a
+// short dense cache): wave w steps tiles w and w + 8 (at most 16 tiles).
+struct F16LeanArgs {
+  LeanCommon c;
+  const _Float16* k;
+  const _Float16* v;
+  int rows;
+};
+
+__global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
+  extern __shared__ __align__(16) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t head = blockIdx.x;
+  half8 qB[4];
+  lean_prologue<F16LeanArgs>(A.c, head, lane, qB);
+  char* slot = lds + kLdsSlots + wave * kSlotBytes;
+  const size_t off = (size_t)head * A.rows * kHeadDim;
+  const uint32_t bytes = (uint32_t)A.rows * kRowBytes;
+  const rsrc_t rk = make_rsrc(A.k + off, bytes), rv = make_rsrc(A.v + off, bytes);
+  const int n_tiles = (A.rows + kTile - 1) / kTile;
+  // a tile with no valid slot loads nothing (zeros; its step is skipped)
+  auto base = [&](int tile) {
+    return tile < n_tiles && tile_any_valid(A.c.R, kTile * tile) ? (uint32_t)tile * kSlotBytes : kOOB;
+  };
+  WaveState st;
+  wave_state_init(st);
+  if (wave + kWaves < n_tiles) {
+    F16Raw X0, X1;
+    load_f16(rk, rv, base(wave), lane, X0);
+    load_f16(rk, rv, base(wave + kWaves), lane, X1);
+    f16_tile_step(X0, slot, qB, kTile * wave, A.c.R, A.c.scale_log2, st, lane);
+    f16_tile_step(X1, slot, qB, kTile * (wave + kWaves), A.c.R, A.c.scale_log2, st, lane);
+  } else if (wave < n_tiles) {
+    F16Raw X;
+    load_f16(rk, rv, base(wave), lane, X);
+    f16_tile_step(X, slot, qB, kTile * wave, A.c.R, A.c.scale_log2, st, lane);
+  }
+  lean_publish_ml(A.c.G, st, lds, lane, wave);
+  lean_publish_f(A.c.G, st, slot, lane);
+  lean_merge(A.c, lds, head);
+}
+
+// The fused KIVI decode with a 128-row fp16 residual (4 tiles) and at most
+// 8 quantized groups (window-old groups, then the sink group): waves 0..3
+// step quantized groups w and w + 4, waves 4..7 residual tile w - 4.  Wave w
+// and w + 4 share a SIMD, so each SIMD carries one fp16 tile and one or two
+// quantized groups.  The residual waves issue their loads only after a
+// workgroup barrier that the quantized waves reach once theirs are issued: a
+// CU serves its loads roughly in issue order, so the quantized groups' data
+// (their steps are the long ones) arrives first and the fp16 tiles stream in
+// behind it.
+struct KiviLeanArgs {
+  LeanCommon c;
+  const _Float16* kres;  // [heads][128][128]
+  const _Float16* vres;
+  QRegion sinkq;         // head 0
+  QRegion winq;          // head 0
+  int nwt;               // window-old groups (<= 7)
+  int sink;
+};
+
+__global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) {
+  extern __shared__ __align__(16) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t head = blockIdx.x;
+  half8 qB[4];
+  lean_prologue<KiviLeanArgs>(A.c, head, lane, qB);
+  char* slot = lds + kLdsSlots + wave * kSlotBytes;
+  const int nwt = A.nwt, win_tok = kTile * nwt;
+  WaveState st;
+  wave_state_init(st);
+  if (wave < 4) {
+    QRegion S = A.sinkq, Wq = A.winq;
+    S.kp += (size_t)head * 8 * kHeadDim;
+    S.ks += (size_t)head * kHeadDim;
+    S.kz += (size_t)head * kHeadDim;
+    S.vp += (size_t)head * 32 * 32;
+    S.vs += (size_t)head * 32 * 4;
+    S.vz += (size_t)head * 32 * 4;
+    Wq.kp += (size_t)head * nwt * 8 * kHeadDim;
+    Wq.ks += (size_t)head * nwt * kHeadDim;
+    Wq.kz += (size_t)head * nwt * kHeadDim;
+    Wq.vp += (size_t)head * nwt * 32 * 32;
+    Wq.vs += (size_t)head * nwt * 32 * 4;
+    Wq.vz += (size_t)head * nwt * 32 * 4;
+    const int n_q = nwt + 1;
+    // item i < nwt: window-old group i (slots sink + 32 i ..); item nwt: the
+    // sink group (`sink` real tokens at slots 0 ..); past n_q: nothing
+    auto load = [&](int i, QTileRaw& X) {
+      const bool sk = i == nwt;
+      load_q_raw(sk ? S : Wq, sk ? 0 : i, i < n_q, lane, X);
+    };
+    QState qs;
+    q_state_init(qs);
+    QTileRaw X0, X1;
+    load(wave, X0);
+    load(wave + 4, X1);
+    __syncthreads();
+    auto step = [&](int i, const QTileRaw& X) {
+      const bool sk = i == nwt;
+      q_tile_step<false>(X, slot, qB, sk ? 0 : A.sink + kTile * i, sk ? A.sink : kTile, A.c.R,
+                         A.c.scale_log2, st, qs, lane);
+    };
+    if (wave < n_q) step(wave, X0);
+    if (wave + 4 < n_q) step(wave + 4, X1);
+    lean_publish_ml(A.c.G, st, lds, lane, wave);
+    publish_q<false>(qs, slot, lane);
+  } else {
+    const int tile = wave - 4;
+    const int slot0 = A.sink + win_tok + kTile * tile;
+    const size_t off = (size_t)head * 128 * kHeadDim;
+    const rsrc_t rk = make_rsrc(A.kres + off, 128 * kRowBytes), rv = make_rsrc(A.vres + off, 128 * kRowBytes);
+    F16Raw X;
+    __syncthreads();
+    load_f16(rk, rv, tile_any_valid(A.c.R, slot0) ? (uint32_t)tile * kSlotBytes : kOOB, lane, X);
+    f16_tile_step(X, slot, qB, slot0, A.c.R, A.c.scale_log2, st, lane);
+    lean_publish_ml(A.c.G, st, lds, lane, wave);
+    lean_publish_f(A.c.G, st, slot, lane);
+  }
+  lean_merge(A.c, lds, head);
+}
+
 // Log-sum-exp merge of the split partials: one thread per output element.
 __global__ __launch_bounds__(256) void merge_kernel(AttnCommon P) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -920,6 +1134,35 @@ int launch_attn(AttnCommon P, const Src& S, bool kivi, size_t ws_bytes, hipStrea
   return launch_status();
 }
 
+// The lean kernels' launches (one workgroup per KV head).
+LeanCommon lean_common(const AttnCommon& P) {
+  LeanCommon C;
+  C.q = P.q;
+  C.o = P.o;
+  C.scale_log2 = P.scale_log2;
+  C.G = P.G;
+  C.R = P.R;
+  return C;
+}
+
+// A contiguous fp16 source qualifies when one pass suffices and no wave has
+// more than two tiles.
+bool f16_lean_fits(const AttnCommon& P) {
+  return make_plan(P.pairs, P.n_tiles).splits == 1 && P.n_tiles <= 2 * kWaves &&
+         P.pairs <= 0x7fffffffLL;
+}
+
+int launch_f16_lean(const AttnCommon& P, const _Float16* k, const _Float16* v, int rows,
+                    hipStream_t stream) {
+  F16LeanArgs A;
+  A.c = lean_common(P);
+  A.k = k;
+  A.v = v;
+  A.rows = rows;
+  hipLaunchKernelGGL(f16_lean_kernel, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, stream, A);
+  return launch_status();
+}
+
 // The fused KIVI decode at one length (lens null) or at per-sequence
 // lengths lens[b] (seq_len unused).
 // Device address of `scratch` on the current device, looked up once per
@@ -1012,6 +1255,18 @@ int kivi_decode(const void* q, const void* k_res, const void* v_res, const void*
   S.window = window;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (lens) return launch_attn(P, S, true, 0, st);
+  if (res_rows == 4 * kTile && S.nwt + 1 <= 2 * 4 && P.pairs <= 0x7fffffffLL) {
+    KiviLeanArgs A;
+    A.c = lean_common(P);
+    A.kres = S.kres;
+    A.vres = S.vres;
+    A.sinkq = S.sinkq;
+    A.winq = S.winq;
+    A.nwt = S.nwt;
+    A.sink = sink;
+    hipLaunchKernelGGL(kivi_lean_kernel, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, st, A);
+    return launch_status();
+  }
   KiviSrc S1{};
   S1.kres = S.kres;
   S1.vres = S.vres;
@@ -1219,6 +1474,9 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int
   P.n_tiles = (int)tiles_for(KVDEC_KIND_DENSE, L);
   P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
   P.R = SlotRanges{(int)L, 0, 0};
+  if (f16_lean_fits(P))
+    return launch_f16_lean(P, static_cast<const _Float16*>(k), static_cast<const _Float16*>(v), (int)L,
+                           static_cast<hipStream_t>(stream));
   F16Src S{static_cast<const _Float16*>(k), static_cast<const _Float16*>(v), (int)L};
   return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
 }
@@ -1263,6 +1521,9 @@ int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
   P.n_tiles = (int)tiles_for(KVDEC_KIND_SPARSE, n);
   P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
   P.R = sparse_ranges(seq_len, window, sink, layout);
+  if (f16_lean_fits(P))
+    return launch_f16_lean(P, static_cast<const _Float16*>(k_cache), static_cast<const _Float16*>(v_cache),
+                           (int)n, static_cast<hipStream_t>(stream));
   F16Src S{static_cast<const _Float16*>(k_cache), static_cast<const _Float16*>(v_cache), (int)n};
   return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
 }
