@@ -223,40 +223,41 @@ __device__ __forceinline__ void publish_f(const AttnCommon& P, const WaveState& 
   }
 }
 
-// Quantized-tile accumulators: lane (t, g) holds head 4g + r of channel
-// q_state_channel(grp, m, t) in QState::O[2 grp + m], scaled by
-// 1 / q_state_scale().  All 16 head rows are written (rows of heads >= G
-// stay inside the wave's slot and the merge never reads them), so no write
-// is predicated.  ADD: the slot already holds this wave's fp16-tile rows
-// (all reads are issued before any write, so the adds wait on LDS once).
+// Quantized-tile accumulators: lane (t, g) holds head 4g + r of channels
+// q_state_channel(grp, 0..1, t) (adjacent) in QState::O[2 grp + 0..1]; each
+// pair goes out as one 8-byte write.  All 16 head rows are written (rows of heads >= G stay inside the
+// wave's slot and the merge never reads them), so no write is predicated.
+// ADD: the slot already holds this wave's fp16-tile rows (all reads are
+// issued before any write, so the adds wait on LDS once).
 template <bool ADD>
 __device__ __forceinline__ void publish_q(QState& qs, char* slot, int lane) {
   const int t = lane & 15, g = lane >> 4;
-  const float f = q_state_scale();
+  float2v v[4][4];
+  uint32_t off[4][4];
 #pragma unroll
-  for (int blk = 0; blk < 8; ++blk) qs.O[blk] = qs.O[blk] * f;
-  uint32_t off[8][4];
+  for (int grp = 0; grp < 4; ++grp) {
+    const int ch = q_state_channel(grp, 0, t);
 #pragma unroll
-  for (int blk = 0; blk < 8; ++blk) {
-    const int ch = q_state_channel(blk >> 1, blk & 1, t);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) off[blk][r] = row_off(4 * g + r, ch >> 2) + 4 * (ch & 3);
+    for (int r = 0; r < 4; ++r) {
+      off[grp][r] = row_off(4 * g + r, ch >> 2) + 4 * (ch & 3);
+      v[grp][r] = float2v{qs.O[2 * grp][r], qs.O[2 * grp + 1][r]};
+    }
   }
   if (ADD) {
-    float prev[8][4];
+    float2v prev[4][4];
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
+    for (int grp = 0; grp < 4; ++grp)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) prev[blk][r] = *reinterpret_cast<const float*>(slot + off[blk][r]);
+      for (int r = 0; r < 4; ++r) prev[grp][r] = *reinterpret_cast<const float2v*>(slot + off[grp][r]);
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
+    for (int grp = 0; grp < 4; ++grp)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) qs.O[blk][r] += prev[blk][r];
+      for (int r = 0; r < 4; ++r) v[grp][r] += prev[grp][r];
   }
 #pragma unroll
-  for (int blk = 0; blk < 8; ++blk)
+  for (int grp = 0; grp < 4; ++grp)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) *reinterpret_cast<float*>(slot + off[blk][r]) = qs.O[blk][r];
+    for (int r = 0; r < 4; ++r) *reinterpret_cast<float2v*>(slot + off[grp][r]) = v[grp][r];
 }
 
 // Barrier, then combine the waves' published partials into the output (one
@@ -955,21 +956,25 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
 }
 
 // The fused KIVI decode with a 128-row fp16 residual (4 tiles) and at most
-// 8 quantized groups (window-old groups, then the sink group): waves 0..3
-// step quantized groups w and w + 4, waves 4..7 residual tile w - 4.  Wave w
-// and w + 4 share a SIMD, so each SIMD carries one fp16 tile and one or two
-// quantized groups.  The residual waves issue their loads only after a
-// workgroup barrier that the quantized waves reach once theirs are issued: a
-// CU serves its loads roughly in issue order, so the quantized groups' data
-// (their steps are the long ones) arrives first and the fp16 tiles stream in
-// behind it.
+// 7 window-old groups: the quantized items are window-old groups 0..nwt-1
+// and the sink group (item nwt, 4 real tokens, the cheapest step); waves
+// 0..3 step items w and w + 4, waves 4..7 residual tiles 0..3.  Wave w and
+// w + 4 share a SIMD.  Every load goes through a resource over a whole
+// tensor with the KV head's (and group's) offset in the scalar offset
+// field, so no per-head pointer arithmetic precedes the first load.  The
+// residual loads are issued only after a workgroup barrier that the
+// quantized waves reach once their loads are issued: a CU serves its loads
+// roughly in issue order, so the quantized groups' data (their steps are
+// the long ones) arrives first and the fp16 tiles stream in behind it.
 struct KiviLeanArgs {
   LeanCommon c;
   const _Float16* kres;  // [heads][128][128]
   const _Float16* vres;
-  QRegion sinkq;         // head 0
-  QRegion winq;          // head 0
-  int nwt;               // window-old groups (<= 7)
+  QRegion sinkq;         // [heads] groups
+  QRegion winq;          // [heads][nwt] groups
+  uint32_t res_bytes;    // whole-tensor sizes, each < 2^31
+  uint32_t win_code_bytes, win_meta_bytes, sink_code_bytes, sink_meta_bytes;
+  int nwt;               // window-old groups (<= 8)
   int sink;
 };
 
@@ -981,32 +986,20 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
   half8 qB[4];
   lean_prologue<KiviLeanArgs>(A.c, head, lane, qB);
   char* slot = lds + kLdsSlots + wave * kSlotBytes;
-  const int nwt = A.nwt, win_tok = kTile * nwt;
+  const int nwt = A.nwt;
   WaveState st;
   wave_state_init(st);
   if (wave < 4) {
-    QRegion S = A.sinkq, Wq = A.winq;
-    S.kp += (size_t)head * 8 * kHeadDim;
-    S.ks += (size_t)head * kHeadDim;
-    S.kz += (size_t)head * kHeadDim;
-    S.vp += (size_t)head * 32 * 32;
-    S.vs += (size_t)head * 32 * 4;
-    S.vz += (size_t)head * 32 * 4;
-    Wq.kp += (size_t)head * nwt * 8 * kHeadDim;
-    Wq.ks += (size_t)head * nwt * kHeadDim;
-    Wq.kz += (size_t)head * nwt * kHeadDim;
-    Wq.vp += (size_t)head * nwt * 32 * 32;
-    Wq.vs += (size_t)head * nwt * 32 * 4;
-    Wq.vz += (size_t)head * nwt * 32 * 4;
-    const int n_q = nwt + 1;
-    // item i < nwt: window-old group i (slots sink + 32 i ..); item nwt: the
-    // sink group (`sink` real tokens at slots 0 ..); past n_q: nothing
-    auto load = [&](int i, QTileRaw& X) {
-      const bool sk = i == nwt;
-      load_q_raw(sk ? S : Wq, sk ? 0 : i, i < n_q, lane, X);
-    };
     QState qs;
     q_state_init(qs);
+    const int n_q = nwt + 1;
+    // item i < nwt: window-old group i; item nwt: the sink group
+    auto load = [&](int i, QTileRaw& X) {
+      const bool sk = i == nwt;
+      const QTensors T = sk ? q_tensors(A.sinkq, A.sink_code_bytes, A.sink_meta_bytes)
+                            : q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
+      load_q_group(T, sk ? head : head * (uint32_t)nwt + (uint32_t)i, i < n_q, lane, X);
+    };
     QTileRaw X0, X1;
     load(wave, X0);
     load(wave + 4, X1);
@@ -1022,12 +1015,13 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     publish_q<false>(qs, slot, lane);
   } else {
     const int tile = wave - 4;
-    const int slot0 = A.sink + win_tok + kTile * tile;
-    const size_t off = (size_t)head * 128 * kHeadDim;
-    const rsrc_t rk = make_rsrc(A.kres + off, 128 * kRowBytes), rv = make_rsrc(A.vres + off, 128 * kRowBytes);
+    const int slot0 = A.sink + kTile * nwt + kTile * tile;
+    const rsrc_t rk = make_rsrc(A.kres, A.res_bytes), rv = make_rsrc(A.vres, A.res_bytes);
+    const uint32_t soff = head * (uint32_t)(128 * kRowBytes);
+    const uint32_t base = tile_any_valid(A.c.R, slot0) ? (uint32_t)tile * kSlotBytes : kOOB;
     F16Raw X;
     __syncthreads();
-    load_f16(rk, rv, tile_any_valid(A.c.R, slot0) ? (uint32_t)tile * kSlotBytes : kOOB, lane, X);
+    load_f16(rk, rv, base, soff, lane, X);
     f16_tile_step(X, slot, qB, slot0, A.c.R, A.c.scale_log2, st, lane);
     lean_publish_ml(A.c.G, st, lds, lane, wave);
     lean_publish_f(A.c.G, st, slot, lane);
@@ -1255,13 +1249,21 @@ int kivi_decode(const void* q, const void* k_res, const void* v_res, const void*
   S.window = window;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (lens) return launch_attn(P, S, true, 0, st);
-  if (res_rows == 4 * kTile && S.nwt + 1 <= 2 * 4 && P.pairs <= 0x7fffffffLL) {
+  // the lean kernel: 4 residual tiles, at most 8 window-old groups, and
+  // every tensor small enough for 31-bit offsets
+  const int64_t lean_bytes = P.pairs * (int64_t)(128 * kRowBytes);
+  if (res_rows == 4 * kTile && S.nwt + 1 <= 2 * 4 && lean_bytes < ((int64_t)1 << 31)) {
     KiviLeanArgs A;
     A.c = lean_common(P);
     A.kres = S.kres;
     A.vres = S.vres;
     A.sinkq = S.sinkq;
     A.winq = S.winq;
+    A.res_bytes = (uint32_t)lean_bytes;
+    A.win_code_bytes = (uint32_t)(P.pairs * S.nwt * 1024);
+    A.win_meta_bytes = (uint32_t)(P.pairs * S.nwt * 256);
+    A.sink_code_bytes = (uint32_t)(P.pairs * 1024);
+    A.sink_meta_bytes = (uint32_t)(P.pairs * 256);
     A.nwt = S.nwt;
     A.sink = sink;
     hipLaunchKernelGGL(kivi_lean_kernel, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, st, A);

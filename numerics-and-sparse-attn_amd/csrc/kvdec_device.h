@@ -33,6 +33,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -64,15 +65,18 @@ __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kStreamAux);
 }
 
+// The same with a wave-uniform byte offset `soff` added (an SGPR operand,
+// outside the range check, which applies to `off`: an `off` of kOOB still
+// reads zeros without a memory access).
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, kStreamAux);
+}
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, soff, kStreamAux);
+}
+
 __device__ __forceinline__ half8 as_h8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 __device__ __forceinline__ u32x4 as_u4(half8 v) { return __builtin_bit_cast(u32x4, v); }
-
-// a - b on the two fp16 halves of a dword.  Written as a 2-wide vector
-// subtraction on its own so it stays one v_pk_add_f16 (subtracting 8-wide
-// vectors is split into scalar halves by the compiler).
-__device__ __forceinline__ uint32_t pk_sub_f16(uint32_t a, uint32_t b) {
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) - __builtin_bit_cast(half2v, b));
-}
 
 // Sum / max over the four lanes t, t + 16, t + 32, t + 48 (the lane groups g
 // of one MFMA row), left in all four.  Each step swaps rows between two
@@ -276,6 +280,17 @@ __device__ __forceinline__ void load_f16(rsrc_t rk, rsrc_t rv, uint32_t base, in
   for (int j = 0; j < 8; ++j) X.v[j] = bload16(rv, base + (uint32_t)tau(g, j) * kRowBytes + 16u * t);
 }
 
+// load_f16 against a resource over a whole tensor, the KV head's region
+// starting `soff` bytes in.
+__device__ __forceinline__ void load_f16(rsrc_t rk, rsrc_t rv, uint32_t base, uint32_t soff, int lane,
+                                         F16Raw& X) {
+  const uint32_t t = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) X.k[i] = bload16(rk, base + (4u * i + g) * kRowBytes + 16u * t, soff);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) X.v[j] = bload16(rv, base + (uint32_t)tau(g, j) * kRowBytes + 16u * t, soff);
+}
+
 // LDS byte offset of 16-byte chunk `chunk` of K row `row` inside a wave slot:
 // chunks are XOR-swizzled by the row so that both the row-wise stores and
 // the column-wise MFMA operand reads hit 16 distinct bank groups.
@@ -335,6 +350,31 @@ struct QTileRaw {
   uint32_t vs, vz;     // V scale / zero of token L/2, groups 2(L%2), 2(L%2)+1
 };
 
+// Resources over the six whole tensors of a KIVI region (all KV heads):
+// every 32-token group is 1024 bytes of K codes and of V codes and 256 bytes
+// of each scale / zero piece, so group n starts at n * 1024 and n * 256.
+struct QTensors {
+  rsrc_t kc, vc, ks, kz, vs, vz;
+};
+
+__device__ __forceinline__ QTensors q_tensors(const QRegion& Q, uint32_t code_bytes, uint32_t meta_bytes) {
+  return QTensors{make_rsrc(Q.kp, code_bytes), make_rsrc(Q.vp, code_bytes), make_rsrc(Q.ks, meta_bytes),
+                  make_rsrc(Q.kz, meta_bytes), make_rsrc(Q.vs, meta_bytes), make_rsrc(Q.vz, meta_bytes)};
+}
+
+// Issue the loads of group n of the tensors (valid == false: zeros, no
+// access); the group's offsets go in the scalar offset field.
+__device__ __forceinline__ void load_q_group(const QTensors& T, uint32_t n, bool valid, int lane, QTileRaw& X) {
+  const uint32_t oc = n * 1024u, om = n * 256u;
+  const uint32_t l16 = valid ? 16u * lane : kOOB, l4 = valid ? 4u * lane : kOOB;
+  X.kc = bload16(T.kc, l16, oc);
+  X.vc = bload16(T.vc, l16, oc);
+  X.ks = bload4(T.ks, l4, om);
+  X.kz = bload4(T.kz, l4, om);
+  X.vs = bload4(T.vs, l4, om);
+  X.vz = bload4(T.vz, l4, om);
+}
+
 // Issue the loads of tile tq of region Q (valid == false: zeros, no access).
 __device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, bool valid, int lane,
                                            QTileRaw& X) {
@@ -350,15 +390,14 @@ __device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, bool valid,
 
 // Accumulators of the KIVI tiles, kept beside WaveState (whose m and l they
 // share).  The PV product of a quantized tile is computed transposed,
-// O[head][channel] = P'[head][token] . (code - zero)[token][channel], with
-// each MFMA covering 16 channels of one 32-channel V quantization group, so
-// the per-token V scale folds into P' = p * scale.  The B operand is
-// (code - zero) * 2^-8: exact normal fp16 values (the MFMA rounds products
-// of fp16 subnormals to about 2^-13, so the operand is kept out of the
-// subnormal range).
-//   O[2 grp + m][r] : 2^-8 sum_t P'[t][head 4g + r] * (code - zero)[t][ch]
-//                     for lane (t, g), channel ch = 32 grp + 4 (t & 7) +
-//                     2 m + (t >> 3); q_state_scale() is 2^8
+// O[head][channel] = P'[head][token] . code[token][channel], with each MFMA
+// covering 16 channels of one 32-channel V quantization group, so the
+// per-token V scale folds into P' = p * scale.  The zero point is a
+// separate product, sum_t P'[t] (code - zero) = sum_t P' code + sum_t P'
+// (-zero), accumulated into the same block: both products are exact (codes
+// 0..3 and the integer zeros are exact fp16 operands).
+//   O[2 grp + m][r] : sum_t P'[t][head 4g + r] * (code - zero)[t][ch] for
+//                     lane (t, g), channel ch = q_state_channel(grp, m, t)
 struct QState {
   float4v O[8];
 };
@@ -368,12 +407,10 @@ __device__ __forceinline__ void q_state_init(QState& qs) {
   for (int b = 0; b < 8; ++b) qs.O[b] = float4v{0.f, 0.f, 0.f, 0.f};
 }
 
-// Factor that turns the accumulators into output values.
-__device__ __forceinline__ float q_state_scale() { return 256.0f; }
-
-// Output channel of accumulator column t of QState::O[2 grp + m].
+// Output channel of accumulator column t of QState::O[2 grp + m]: the two
+// accumulators of a group hold adjacent channels.
 __device__ __forceinline__ int q_state_channel(int grp, int m, int t) {
-  return 32 * grp + 4 * (t & 7) + 2 * m + (t >> 3);
+  return 32 * grp + 4 * (t & 7) + 2 * (t >> 3) + m;
 }
 
 // Rescale by alpha, given per head in lane layout (head = lane & 15); the
@@ -389,27 +426,27 @@ __device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lan
 
 // Layout of a staged KIVI tile inside a wave slot (bytes):
 //   [0, 1024)     K codes, 8 byte rows x 128 channels (as stored)
-//   [1024, 1280)  K scales [128], [1280, 1536) 1024 + K zeros [128]
+//   [1024, 1280)  K scales [128], [1280, 1536) negated K zeros [128]
 //   [1536, 2560)  V codes, 32 token rows x 32 bytes (as stored; read back
 //                 transposed by ds_read_b64_tr_b8)
 //   [2560, 2816)  V scales transposed [4 groups][32 tokens],
-//   [2816, 3072)  V zeros transposed
-//   [3072, 3328)  K zeros [128] as stored (the exact-zero path)
-constexpr int kQsK = 0, kQsKS = 1024, kQsKZ = 1280, kQsV = 1536, kQsVS = 2560, kQsVZ = 2816,
-              kQsKZr = 3072;
+//   [2816, 3072)  negated V zeros transposed
+constexpr int kQsK = 0, kQsKS = 1024, kQsKZ = 1280, kQsV = 1536, kQsVS = 2560, kQsVZ = 2816;
+constexpr int kQsBytes = 3072;
+constexpr uint32_t kNegPk = 0x80008000u;   // sign bits of an fp16 pair
 
 __device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
   *reinterpret_cast<u32x4*>(slot + kQsK + 16 * lane) = X.kc;
   *reinterpret_cast<uint32_t*>(slot + kQsKS + 4 * lane) = X.ks;
-  *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = pk_sub_f16(X.kz, 0xe400e400u);   // + 1024
-  *reinterpret_cast<uint32_t*>(slot + kQsKZr + 4 * lane) = X.kz;
+  *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = X.kz ^ kNegPk;
   *reinterpret_cast<u32x4*>(slot + kQsV + 16 * lane) = X.vc;
   // lane L holds the scale / zero of token L/2, groups 2(L%2) and 2(L%2)+1
   const int tok = lane >> 1, g0 = 2 * (lane & 1);
+  const uint32_t nvz = X.vz ^ kNegPk;
   *reinterpret_cast<uint16_t*>(slot + kQsVS + g0 * 64 + 2 * tok) = (uint16_t)X.vs;
   *reinterpret_cast<uint16_t*>(slot + kQsVS + (g0 + 1) * 64 + 2 * tok) = (uint16_t)(X.vs >> 16);
-  *reinterpret_cast<uint16_t*>(slot + kQsVZ + g0 * 64 + 2 * tok) = (uint16_t)X.vz;
-  *reinterpret_cast<uint16_t*>(slot + kQsVZ + (g0 + 1) * 64 + 2 * tok) = (uint16_t)(X.vz >> 16);
+  *reinterpret_cast<uint16_t*>(slot + kQsVZ + g0 * 64 + 2 * tok) = (uint16_t)nvz;
+  *reinterpret_cast<uint16_t*>(slot + kQsVZ + (g0 + 1) * 64 + 2 * tok) = (uint16_t)(nvz >> 16);
 }
 
 // Transposed LDS read (gfx950 ds_read_b64_tr_b8).  In each group of 16
@@ -432,17 +469,34 @@ __device__ __forceinline__ uint32_t fma_mix_pk_f16(float a0, float a1, uint32_t 
   return d;
 }
 
-// Two codes of `c` (one code per byte; sel 0x00050004 takes bytes 0 and 1,
-// 0x00070006 bytes 2 and 3) as the fp16 pair (1024 + code_a, 1024 + code_b):
-// the patterns 0x6400 | code.
-__device__ __forceinline__ uint32_t codes_1024(uint32_t c, uint32_t sel) {
-  return __builtin_amdgcn_perm(c, 0x64646464u, sel);
+// Four 2-bit codes, one in bits 0..1 of each byte of `c` (the other bits
+// zero), as four exact fp16 values: such a byte is the OCP fp8 e4m3
+// subnormal code * 2^-9, which v_cvt_scalef32_pk_f16_fp8 widens and scales
+// by `scale` in one step per pair of bytes.
+__device__ __forceinline__ u32x2 codes_f16(uint32_t c, float scale) {
+  return u32x2{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c, scale, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c, scale, true))};
+}
+constexpr float kCodeScale = 512.0f;   // code * 2^-9 * 2^9 = code
+
+// The 2-bit fields at bit `sh` of every byte of the 8 bytes w, one per byte.
+// One 64-bit shift: bits that cross from w[1] into w[0] land above bit 1 of
+// byte 3 and are masked off.
+__device__ __forceinline__ u32x2 fields2(u32x2 w, uint32_t sh) {
+  const uint64_t x = ((uint64_t)w[1] << 32 | w[0]) >> sh;
+  return u32x2{(uint32_t)x & 0x03030303u, (uint32_t)(x >> 32) & 0x03030303u};
 }
 
 // Consume one KIVI tile staged in the wave's LDS slot.
-//   QK: fp16 patterns 0x6400 | code are 1024 + code exactly; adding
-//       -(1024 + zero) gives code - zero exactly (the A operand), and the
-//       per-channel K scale goes to the Q side (see below).
+//   QK: the codes are exact fp16 integers (A operand); the per-channel K
+//       scale goes to the Q side as q * scale = head + remainder, both fp16
+//       (the remainder of an fp16 x fp16 product is exact in fp16), so the
+//       logits carry the dequantized K exactly instead of fp16 roundings of
+//       scale * (code - zero).  The zero point adds -sum_ch zero[ch] *
+//       q[ch] * scale[ch] to every token of a head: one extra 16x16 block
+//       (the negated zeros, the same in every row, against the same head
+//       and remainder of q * scale), so all its rows hold that term and it
+//       enters the logits in the fused multiply-add that scales them.
 //   softmax: the reference max is refreshed when the tile's max exceeds it
 //       by more than `slack`: kRescaleSlack when every V scale of the tile
 //       is at most kSlackVScale (then p <= 2^8 and P' = p * vscale < 2^15
@@ -452,63 +506,39 @@ __device__ __forceinline__ uint32_t codes_1024(uint32_t c, uint32_t sel) {
 // Without MIXED, st.O must be zero.  HALF: only tokens 0..15 can be valid (the sink
 // group), so the second 16-token block is skipped in QK and fed as zeros to
 // PV.  Masked tokens get p = 0; their codes are finite.
-//   FOLD: every V zero of the tile has |zero| <= kFoldZeroMax, so
-//       (code - zero) * 4^k * 2^-8 is one exact fp16 (one MFMA pair per
-//       16 channels), and every K zero has |zero| <= kFoldKZeroMax, so
-//       1024 + zero and code - zero are exact fp16 integers.  Otherwise
-//       codes and zeros go through separate MFMAs: V as below, K as the
-//       exact codes against q * scale plus one zero term per head,
-//       -sum_ch zero[ch] * q[ch] * scale[ch] (the same for every token),
-//       taken from the zeros as stored (fp16, exact) against the same
-//       head and remainder of q * scale.
 constexpr float kSlackVScale = 128.0f;
-constexpr float kFoldZeroMax = 1000.0f;
-constexpr float kFoldKZeroMax = 1024.0f;
 
-template <bool MIXED, bool HALF, bool FOLD>
+template <bool MIXED, bool HALF>
 __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[4], int slot0,
                                             int xlim, const SlotRanges& R, float scale_log2,
                                             float slack, WaveState& st, QState& qs, int lane) {
   const int t = lane & 15, g = lane >> 4;
-  // scale and 1024 + zero of the lane's K channels 32c + 8g .. +7
-  half8 ks[4];
-  u32x4 kz1[4];
+  // scale and negated zero of the lane's K channels 32c + 8g .. +7
+  half8 ks[4], nz[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     ks[c] = *reinterpret_cast<const half8*>(slot + kQsKS + 2 * (32 * c + 8 * g));
-    kz1[c] = *reinterpret_cast<const u32x4*>(slot + kQsKZ + 2 * (32 * c + 8 * g));
+    nz[c] = *reinterpret_cast<const half8*>(slot + kQsKZ + 2 * (32 * c + 8 * g));
   }
 
   // S[token][head] on MFMA: lane (t, g) feeds token 16 blk + t, channels
-  // 32c + 8g .. +7 (code byte row (16 blk + t) / 4, bits 2 (t % 4)) as the
-  // exact small integer code - zero; the per-channel K scale goes to the Q
-  // side as q * scale = head + remainder, both fp16 (the remainder of an
-  // fp16 x fp16 product is exact in fp16), so the logits carry the
-  // dequantized K exactly instead of fp16 roundings of scale * (code - zero).
+  // 32c + 8g .. +7 (code byte row (16 blk + t) / 4, bits 2 (t % 4)).
   const uint32_t sh = 2u * (uint32_t)(t & 3);
   float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-  float4v sz = {0.f, 0.f, 0.f, 0.f};   // !FOLD: the zero term of every token row
+  float4v sz = {0.f, 0.f, 0.f, 0.f};   // the zero term of every token row
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const half8 qh = qB[c] * ks[c];
     const half8 ql = __builtin_elementwise_fma(qB[c], ks[c], -qh);
-    if (!FOLD) {
-      const half8 nz = -*reinterpret_cast<const half8*>(slot + kQsKZr + 2 * (32 * c + 8 * g));
-      sz = mfma16x16x32(as_u4(nz), qh, sz);
-      sz = mfma16x16x32(as_u4(nz), ql, sz);
-    }
+    sz = mfma16x16x32(as_u4(nz[c]), qh, sz);
+    sz = mfma16x16x32(as_u4(nz[c]), ql, sz);
 #pragma unroll
     for (int blk = 0; blk < (HALF ? 1 : 2); ++blk) {
       const u32x2 w =
           *reinterpret_cast<const u32x2*>(slot + kQsK + (4 * blk + (t >> 2)) * 128 + 32 * c + 8 * g);
-      const uint32_t c0 = (w[0] >> sh) & 0x03030303u;
-      const uint32_t c1 = (w[1] >> sh) & 0x03030303u;
-      // FOLD: (1024 + code) - (1024 + zero); otherwise (1024 + code) - 1024
-      const u32x4 kz = FOLD ? kz1[c] : u32x4{0x64006400u, 0x64006400u, 0x64006400u, 0x64006400u};
-      const u32x4 d = {pk_sub_f16(codes_1024(c0, 0x00050004u), kz[0]),
-                       pk_sub_f16(codes_1024(c0, 0x00070006u), kz[1]),
-                       pk_sub_f16(codes_1024(c1, 0x00050004u), kz[2]),
-                       pk_sub_f16(codes_1024(c1, 0x00070006u), kz[3])};
+      const u32x2 f = fields2(w, sh);
+      const u32x2 d0 = codes_f16(f[0], kCodeScale), d1 = codes_f16(f[1], kCodeScale);
+      const u32x4 d = {d0[0], d0[1], d1[0], d1[1]};
       if (blk == 0) {
         s0 = mfma16x16x32(d, qh, s0);
         s0 = mfma16x16x32(d, ql, s0);
@@ -518,14 +548,10 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
       }
     }
   }
-  if (!FOLD) {
-    s0 += sz;
-    s1 += sz;
-  }
-
+  const float xz = sz[0] * scale_log2;
   float x[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) x[j] = (j < 4 ? s0[j & 3] : s1[j & 3]) * scale_log2;
+  for (int j = 0; j < 8; ++j) x[j] = fmaf(j < 4 ? s0[j & 3] : s1[j & 3], scale_log2, xz);
   if (!(xlim == kTile && tile_fully_valid(R, slot0))) {
     const uint32_t valid = tile_valid_bits(R, slot0, xlim, lane);
 #pragma unroll
@@ -560,20 +586,13 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   // a time.  One transposed LDS read gives lane (t, g) byte column
   // 8 grp + (t & 7) of the tokens tau(g, 0..7) (lane t of each lane group
   // supplies the row of token tau(g, t / 2)); MFMA m takes field
-  // f = 2 m + (t >> 3) of those bytes (channel 32 grp + 4 (t & 7) + f),
-  // shifted down to bits 0..1.  The masked byte in the low byte of 0x64xx
-  // is the fp16 1024 + code; times 2^-8 that is 4 + code * 2^-8, so one
-  // fused multiply-add against 4 + zero * 2^-8 (FOLD) or 4 leaves
-  // (code - zero) * 2^-8 or code * 2^-8, exactly.  P' = p * scale (the
-  // per-token V scale of the group) is taken as an fp16 head pq and the
-  // fp16 remainder pl (as for fp16 tiles); tau(g, 0..3) = 4g..4g+3 and
-  // tau(g, 4..7) = 16 + 4g .. +3 sit contiguously in the transposed
-  // scale and zero rows.
+  // f = 2 (t >> 3) + m of those bytes (channel 32 grp + 4 (t & 7) + f).
+  // P' = p * scale (the per-token V scale of the group) is taken as an fp16
+  // head pq and the fp16 remainder pl (as for fp16 tiles);
+  // tau(g, 0..3) = 4g..4g+3 and tau(g, 4..7) = 16 + 4g .. +3 sit
+  // contiguously in the transposed scale and zero rows.
   const char* vrow = slot + kQsV + 32 * tau(g, t >> 1);
-  const uint32_t vsh[2] = {2u * (uint32_t)(t >> 3), 2u * (uint32_t)(t >> 3) + 4u};
-  const half8 r8 = {0.00390625f, 0.00390625f, 0.00390625f, 0.00390625f,
-                    0.00390625f, 0.00390625f, 0.00390625f, 0.00390625f};   // 2^-8
-  const half8 four = {4, 4, 4, 4, 4, 4, 4, 4};
+  const uint32_t vsh = 4u * (uint32_t)(t >> 3);
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
     const u32x2 s_lo = *reinterpret_cast<const u32x2*>(slot + kQsVS + grp * 64 + 8 * g);
@@ -587,25 +606,19 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
     const u32x4 pq = as_u4(pB * as_h8(vsc));
     const u32x4 pl = {fma_mix_pk_f16(pf[0], pf[1], vsc[0], pq[0]), fma_mix_pk_f16(pf[2], pf[3], vsc[1], pq[1]),
                       fma_mix_pk_f16(pf[4], pf[5], vsc[2], pq[2]), fma_mix_pk_f16(pf[6], pf[7], vsc[3], pq[3])};
-    const half8 zv = as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]});
-    // FOLD: 4 + zero * 2^-8 (exact for |zero| <= kFoldZeroMax); otherwise
-    // -zero * 2^-8 for the separate zero term (exact)
-    const half8 zt = FOLD ? __builtin_elementwise_fma(zv, r8, four) : zv * -r8;
-    const half8 off = FOLD ? zt : four;
+    const half8 nzv = as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]});
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      const uint32_t c0 = (vb[0] >> vsh[m]) & 0x03030303u;
-      const uint32_t c1 = HALF ? 0u : (vb[1] >> vsh[m]) & 0x03030303u;
-      const u32x4 bc = {codes_1024(c0, 0x00050004u), codes_1024(c0, 0x00070006u),
-                        codes_1024(c1, 0x00050004u), codes_1024(c1, 0x00070006u)};
-      const half8 b = __builtin_elementwise_fma(as_h8(bc), r8, -off);
+      const uint32_t s = vsh + 2u * (uint32_t)m;
+      const u32x2 c = HALF ? u32x2{(vb[0] >> s) & 0x03030303u, 0u} : fields2(vb, s);
+      const u32x2 b0 = codes_f16(c[0], kCodeScale);
+      const u32x2 b1 = HALF ? u32x2{0u, 0u} : codes_f16(c[1], kCodeScale);
+      const half8 b = as_h8(u32x4{b0[0], b0[1], b1[0], b1[1]});
       float4v& acc = qs.O[2 * grp + m];
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pq), b, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), b, acc, 0, 0, 0);
-      if (!FOLD) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pq), zt, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), zt, acc, 0, 0, 0);
-      }
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pq), nzv, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), nzv, acc, 0, 0, 0);
     }
   }
 }
@@ -620,23 +633,10 @@ __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
   const half2v vs = __builtin_bit_cast(half2v, raw.vs);
   const float slack =
       __ballot(!(fmaxf((float)vs[0], (float)vs[1]) <= kSlackVScale)) ? 0.0f : kRescaleSlack;
-  // and two of its 128 V zeros and two of its 128 K zeros
-  const half2v vz = __builtin_bit_cast(half2v, raw.vz);
-  const half2v kz = __builtin_bit_cast(half2v, raw.kz);
-  const bool fold =
-      !__ballot(!(fmaxf(fabsf((float)vz[0]), fabsf((float)vz[1])) <= kFoldZeroMax &&
-                  fmaxf(fabsf((float)kz[0]), fabsf((float)kz[1])) <= kFoldKZeroMax));
-  if (fold) {
-    if (xlim <= kTile / 2)
-      q_tile_body<MIXED, true, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
-    else
-      q_tile_body<MIXED, false, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
-  } else {
-    if (xlim <= kTile / 2)
-      q_tile_body<MIXED, true, false>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
-    else
-      q_tile_body<MIXED, false, false>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
-  }
+  if (xlim <= kTile / 2)
+    q_tile_body<MIXED, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+  else
+    q_tile_body<MIXED, false>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
 }
 
 }  // namespace kvdec
