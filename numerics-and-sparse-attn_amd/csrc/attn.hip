@@ -933,22 +933,33 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
   const uint32_t bytes = (uint32_t)A.rows * kRowBytes;
   const rsrc_t rk = make_rsrc(A.k + off, bytes), rv = make_rsrc(A.v + off, bytes);
   const int n_tiles = (A.rows + kTile - 1) / kTile;
-  // a tile with no valid slot loads nothing (zeros; its step is skipped)
-  auto base = [&](int tile) {
-    return tile < n_tiles && tile_any_valid(A.c.R, kTile * tile) ? (uint32_t)tile * kSlotBytes : kOOB;
+  // Tile i belongs to group i / 8 of n = min(8, n_tiles - 8 (i / 8)) tiles,
+  // whose rows it takes four at a time, interleaved with the group's other
+  // tiles (slot == row).  A tile with no valid slot loads nothing.
+  auto rows = [&](int i) {
+    const int grp = i / kWaves, nw = min(kWaves, n_tiles - kWaves * grp);
+    return TileRows{kWaves * kTile * grp + 4 * (i % kWaves), 4 * nw};
   };
+  auto live = [&](int i) { return i < n_tiles && tile_any_valid(A.c.R, rows(i)); };
   WaveState st;
   wave_state_init(st);
   if (wave + kWaves < n_tiles) {
     F16Raw X0, X1;
-    load_f16(rk, rv, base(wave), lane, X0);
-    load_f16(rk, rv, base(wave + kWaves), lane, X1);
-    f16_tile_step(X0, slot, qB, kTile * wave, A.c.R, A.c.scale_log2, st, lane);
-    f16_tile_step(X1, slot, qB, kTile * (wave + kWaves), A.c.R, A.c.scale_log2, st, lane);
+    load_f16(rk, rv, rows(wave), live(wave), 0u, lane, X0);
+    load_f16(rk, rv, rows(wave + kWaves), live(wave + kWaves), 0u, lane, X1);
+    f16_tile_step(X0, slot, qB, rows(wave), A.c.R, A.c.scale_log2, st, lane);
+    f16_tile_step(X1, slot, qB, rows(wave + kWaves), A.c.R, A.c.scale_log2, st, lane);
   } else if (wave < n_tiles) {
+    // a single tile in two phases: its V loads are issued once QK and the
+    // softmax are done, so only the PV follows the last bytes to arrive
     F16Raw X;
-    load_f16(rk, rv, base(wave), lane, X);
-    f16_tile_step(X, slot, qB, kTile * wave, A.c.R, A.c.scale_log2, st, lane);
+    const TileRows T = rows(wave);
+    const bool lv = live(wave);
+    load_f16_k(rk, T, lv, 0u, lane, X);
+    uint32_t valid;
+    const TileProbs P = f16_tile_probs(X, slot, qB, T, A.c.R, A.c.scale_log2, st, lane, valid);
+    load_f16_v(rv, T, after_probs(lv, P), 0u, lane, X);
+    f16_tile_pv(X, P, valid, st);
   }
   lean_publish_ml(A.c.G, st, lds, lane, wave);
   lean_publish_f(A.c.G, st, slot, lane);
@@ -1014,6 +1025,9 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     lean_publish_ml(A.c.G, st, lds, lane, wave);
     publish_q<false>(qs, slot, lane);
   } else {
+    // residual tile w - 4: rows 32 (w - 4) .. + 31 (interleaving the four
+    // tiles' rows, or issuing V after the softmax, measured slower here:
+    // these tiles' data arrives last and their steps end the kernel)
     const int tile = wave - 4;
     const int slot0 = A.sink + kTile * nwt + kTile * tile;
     const rsrc_t rk = make_rsrc(A.kres, A.res_bytes), rv = make_rsrc(A.vres, A.res_bytes);
