@@ -23,6 +23,10 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
   paged     the dense L=163840 cache scattered over 16-token pages in a
             random order (vLLM's [pages, 16, KVH, D] layout), decoded through
             block tables and per-sequence lengths (paged_kernel.py)
+  floor     per-step floors of this box: an empty launch of the decode grid
+            and a plain streaming read of each path's algorithmic bytes
+            (kvdec_read_probe), timed the same way; each path records
+            read_floor_us and frac_of_read_floor
   grid      the reference harness's sweep (benchmark.py:34-169): dense at
             every L of CONTEXT_LENGTHS, sparse at every W of WINDOW_SIZES and
             the fused KIVI decode at W = 32 and every W >= R, with the
@@ -353,7 +357,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--paths", default="kivi,sweep,dense,sparse,quantize,stream,paged,grid")
+    ap.add_argument("--paths", default="kivi,sweep,dense,sparse,quantize,stream,paged,grid,floor")
     ap.add_argument("--sweep-windows", default="32,1024,4096",
                     help="windows of the 'sweep' path (fused KIVI decode, config 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -619,6 +623,42 @@ def main():
             torch.cuda.empty_cache()
         progress("grid kivi done")
 
+    floor = None
+    if "floor" in paths:
+        # what the box itself allows a decode step of each path: an empty
+        # launch of the decode grid, and a plain streaming read of the path's
+        # algorithmic bytes (kvdec_read_probe), timed like the paths
+        import _kvdec as KV
+        sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+
+        def probe_us(nbytes, blocks_list=(256, 1024)):
+            nb = (nbytes + 15) // 16 * 16
+            ns = n_sets(nb) if nb else 1
+            bufs = [torch.empty(max(nb, 16) // 4, dtype=torch.int32, device=dev) for _ in range(ns)]
+            best = None
+            for blocks in blocks_list:
+                def pcall(i, blocks=blocks):
+                    KV.check(KV.lib.kvdec_read_probe(KV.ptr(bufs[i]), nb, KV.ptr(sink), blocks,
+                                                     KV.stream_of(sink)), "read_probe")
+                big = nb > (1 << 30)
+                ms, _ = (graph_time(pcall, ns, Kms, ms_warm, replays=2, min_graph=1) if big
+                         else graph_time(pcall, ns, K, Wu))
+                best = ms if best is None else min(best, ms)
+            del bufs
+            return round(best * 1e3, 3)
+
+        floor = {"note": "per-step floors on this box: launch_us = an empty launch of the decode grid "
+                         "(256 workgroups x 512 threads) in the same graph timing; read_us per path = "
+                         "kvdec_read_probe streaming the path's algorithmic bytes (best of 256 and 1024 "
+                         "workgroups); frac_of_read_floor = read_us / us_per_step",
+                 "launch_us": probe_us(0, (256,))}
+        for name, rec in list(out.items()):
+            if rec.get("alg_bytes"):
+                rec["read_floor_us"] = probe_us(rec["alg_bytes"])
+                rec["frac_of_read_floor"] = round(rec["read_floor_us"] / rec["us_per_step"], 4)
+        torch.cuda.empty_cache()
+        progress("floors done")
+
     if want_cpu:
         cpu["config1_dense_L8192_b1"] = cpu_config1()
 
@@ -651,6 +691,8 @@ def main():
         "cpu_baseline": head_cpu,
         "paths": out,
     }
+    if floor is not None:
+        line["floor"] = floor
     if grid is not None:
         line["grid"] = grid
     if cpu is not None:

@@ -363,6 +363,17 @@ int kvdec_dequant_v_tile(const void* packed, const void* scale,
                          int64_t seq_len, int32_t B, int32_t KVH, int32_t D,
                          int32_t block_n, void* stream);
 
+/*
+ * Measurement probe, no counterpart in the reference: streams `bytes` bytes
+ * (a multiple of 16) from `src` with `blocks` workgroups of 512 threads, each
+ * reading one contiguous share with non-temporal 16-byte loads, and writes
+ * the XOR of each workgroup's share (as 32-bit words) to sink[blockIdx]
+ * (`blocks` uint32 words).  bytes = 0 launches the same grid with no reads:
+ * the per-launch cost.  bench.py times both to state a decode step's floor
+ * on the box it runs on.
+ */
+int kvdec_read_probe(const void* src, int64_t bytes, void* sink, int32_t blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,7 @@ SIGNATURES = {
                                           _i32, _f32, _vp, _sz, _vp]),
     "kvdec_dense_decode_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32,
                                                   _i64, _i32, _f32, _vp]),
+    "kvdec_read_probe": (ctypes.c_int, [_vp, _i64, _vp, _i32, _vp]),
     "kvdec_sparse_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32, _i64,
                                            _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
     "kvdec_paged_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32,

@@ -1043,6 +1043,34 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
   lean_merge(A.c, lds, head);
 }
 
+// Streaming read of `n16` 16-byte words, for the measurement of a decode
+// step's floor at the same launch scale (a workgroup reads one contiguous
+// share, 512 threads x 4 loads in flight, non-temporal as the decode's
+// streams): every workgroup writes the XOR of its share, so the reads stay.
+__global__ __launch_bounds__(kThreads) void read_probe_kernel(const u32x4* src, int64_t n16, uint32_t* sink) {
+  const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+  const int64_t b = (int64_t)blockIdx.x * per;
+  const int64_t e = b + per < n16 ? b + per : n16;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int64_t i = b + threadIdx.x; i < e; i += 4 * kThreads) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i + u * kThreads < e) acc ^= __builtin_nontemporal_load(src + i + u * kThreads);
+  }
+  uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  __shared__ uint32_t red[kWaves];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v ^= (uint32_t)__shfl_xor((int)v, off);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) r ^= red[w];
+    sink[blockIdx.x] = r;
+  }
+}
+
 // Log-sum-exp merge of the split partials: one thread per output element.
 __global__ __launch_bounds__(256) void merge_kernel(AttnCommon P) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1495,6 +1523,14 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int
                            static_cast<hipStream_t>(stream));
   F16Src S{static_cast<const _Float16*>(k), static_cast<const _Float16*>(v), (int)L};
   return launch_attn(P, S, false, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int kvdec_read_probe(const void* src, int64_t bytes, void* sink, int32_t blocks, void* stream) {
+  if (!sink || (bytes > 0 && !src)) return KVDEC_E_NULL;
+  if (bytes < 0 || bytes % 16 != 0 || blocks < 1 || blocks > 65536) return KVDEC_E_SHAPE;
+  hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(src), bytes / 16, static_cast<uint32_t*>(sink));
+  return launch_status();
 }
 
 int kvdec_dense_decode_noalloc(const void* q, const void* k, const void* v, void* o, int dtype,

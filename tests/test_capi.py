@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 21
+    assert len(funcs) == 22
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -123,6 +123,17 @@ def test_dense_noalloc_validation():
     assert call(D=64) == E["SHAPE"]
     assert call(L=0) == E["SEQLEN"]
     assert call(L=1 << 23) == E["SHAPE"]
+
+
+def test_read_probe_validation():
+    """The bandwidth probe rejects bad sizes before launching anything."""
+    probe = K.lib.kvdec_read_probe
+    assert probe(FAKE, 1024, None, 256, None) == E["NULL"]
+    assert probe(None, 1024, FAKE, 256, None) == E["NULL"]
+    assert probe(FAKE, 1000, FAKE, 256, None) == E["SHAPE"]
+    assert probe(FAKE, -16, FAKE, 256, None) == E["SHAPE"]
+    assert probe(FAKE, 1024, FAKE, 0, None) == E["SHAPE"]
+    assert probe(FAKE, 1024, FAKE, 65537, None) == E["SHAPE"]
 
 
 def _sparse(**kw):
