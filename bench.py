@@ -25,8 +25,8 @@ scaled x10.  A "step" is one decode call of a path over the whole batch:
             block tables and per-sequence lengths (paged_kernel.py)
   floor     per-step floors of this box: an empty launch of the decode grid
             and a plain streaming read of each path's algorithmic bytes
-            (kvdec_read_probe), timed the same way; each path records
-            read_floor_us and frac_of_read_floor
+            (kvdec_read_probe, best of 512 and 1024 workgroups), timed the
+            same way; each path records read_floor_us and frac_of_read_floor
   grid      the reference harness's sweep (benchmark.py:34-169): dense at
             every L of CONTEXT_LENGTHS, sparse at every W of WINDOW_SIZES and
             the fused KIVI decode at W = 32 and every W >= R, with the
@@ -631,7 +631,7 @@ def main():
         import _kvdec as KV
         sink = torch.zeros(1024, dtype=torch.int32, device=dev)
 
-        def probe_us(nbytes, blocks_list=(256, 1024)):
+        def probe_us(nbytes, blocks_list=(512, 1024)):
             nb = (nbytes + 15) // 16 * 16
             ns = n_sets(nb) if nb else 1
             bufs = [torch.empty(max(nb, 16) // 4, dtype=torch.int32, device=dev) for _ in range(ns)]
@@ -648,9 +648,9 @@ def main():
             return round(best * 1e3, 3)
 
         floor = {"note": "per-step floors on this box: launch_us = an empty launch of the decode grid "
-                         "(256 workgroups x 512 threads) in the same graph timing; read_us per path = "
-                         "kvdec_read_probe streaming the path's algorithmic bytes (best of 256 and 1024 "
-                         "workgroups); frac_of_read_floor = read_us / us_per_step",
+                         "(256 workgroups x 512 threads) in the same graph timing; read_floor_us per path = "
+                         "kvdec_read_probe streaming the path's algorithmic bytes (best of 512 and 1024 "
+                         "workgroups); frac_of_read_floor = read_floor_us / us_per_step",
                  "launch_us": probe_us(0, (256,))}
         for name, rec in list(out.items()):
             if rec.get("alg_bytes"):

@@ -966,10 +966,11 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
   lean_merge(A.c, lds, head);
 }
 
-// The fused KIVI decode with a 128-row fp16 residual (4 tiles) and at most
+// The fused KIVI decode with an fp16 residual of at most 128 rows (4 tiles;
+// fewer when the window is shorter than the residual size) and at most
 // 7 window-old groups: the quantized items are window-old groups 0..nwt-1
 // and the sink group (item nwt, 4 real tokens, the cheapest step); waves
-// 0..3 step items w and w + 4, waves 4..7 residual tiles 0..3.  Wave w and
+// 0..3 step items w and w + 4, waves 4..7 residual tiles 0..3 (if any).  Wave w and
 // w + 4 share a SIMD.  Every load goes through a resource over a whole
 // tensor with the KV head's (and group's) offset in the scalar offset
 // field, so no per-head pointer arithmetic precedes the first load.  The
@@ -979,13 +980,14 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
 // the long ones) arrives first and the fp16 tiles stream in behind it.
 struct KiviLeanArgs {
   LeanCommon c;
-  const _Float16* kres;  // [heads][128][128]
+  const _Float16* kres;  // [heads][res_rows][128]
   const _Float16* vres;
   QRegion sinkq;         // [heads] groups
   QRegion winq;          // [heads][nwt] groups
   uint32_t res_bytes;    // whole-tensor sizes, each < 2^31
+  int res_rows;          // residual rows per KV head (<= 128)
   uint32_t win_code_bytes, win_meta_bytes, sink_code_bytes, sink_meta_bytes;
-  int nwt;               // window-old groups (<= 8)
+  int nwt;               // window-old groups (<= 7)
   int sink;
 };
 
@@ -1031,12 +1033,17 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     const int tile = wave - 4;
     const int slot0 = A.sink + kTile * nwt + kTile * tile;
     const rsrc_t rk = make_rsrc(A.kres, A.res_bytes), rv = make_rsrc(A.vres, A.res_bytes);
-    const uint32_t soff = head * (uint32_t)(128 * kRowBytes);
-    const uint32_t base = tile_any_valid(A.c.R, slot0) ? (uint32_t)tile * kSlotBytes : kOOB;
+    const uint32_t soff = head * (uint32_t)(A.res_rows * kRowBytes);
+    // residual rows past res_rows (the next KV head's, or past the tensor)
+    // are slots past the window: masked, their V rows read as zeros
+    const bool has = tile * kTile < A.res_rows;
+    const uint32_t base = has && tile_any_valid(A.c.R, slot0) ? (uint32_t)tile * kSlotBytes : kOOB;
     F16Raw X;
     __syncthreads();
-    load_f16(rk, rv, base, soff, lane, X);
-    f16_tile_step(X, slot, qB, slot0, A.c.R, A.c.scale_log2, st, lane);
+    if (has) {
+      load_f16(rk, rv, base, soff, lane, X);
+      f16_tile_step(X, slot, qB, slot0, A.c.R, A.c.scale_log2, st, lane);
+    }
     lean_publish_ml(A.c.G, st, lds, lane, wave);
     lean_publish_f(A.c.G, st, slot, lane);
   }
@@ -1291,10 +1298,10 @@ int kivi_decode(const void* q, const void* k_res, const void* v_res, const void*
   S.window = window;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (lens) return launch_attn(P, S, true, 0, st);
-  // the lean kernel: 4 residual tiles, at most 8 window-old groups, and
-  // every tensor small enough for 31-bit offsets
-  const int64_t lean_bytes = P.pairs * (int64_t)(128 * kRowBytes);
-  if (res_rows == 4 * kTile && S.nwt + 1 <= 2 * 4 && lean_bytes < ((int64_t)1 << 31)) {
+  // the lean kernel: at most 4 residual tiles, at most 7 window-old groups,
+  // and every tensor small enough for 31-bit offsets
+  const int64_t lean_bytes = P.pairs * (int64_t)res_rows * kRowBytes;
+  if (res_rows <= 4 * kTile && S.nwt + 1 <= 2 * 4 && lean_bytes < ((int64_t)1 << 31)) {
     KiviLeanArgs A;
     A.c = lean_common(P);
     A.kres = S.kres;
@@ -1302,6 +1309,7 @@ int kivi_decode(const void* q, const void* k_res, const void* v_res, const void*
     A.sinkq = S.sinkq;
     A.winq = S.winq;
     A.res_bytes = (uint32_t)lean_bytes;
+    A.res_rows = res_rows;
     A.win_code_bytes = (uint32_t)(P.pairs * S.nwt * 1024);
     A.win_meta_bytes = (uint32_t)(P.pairs * S.nwt * 256);
     A.sink_code_bytes = (uint32_t)(P.pairs * 1024);
