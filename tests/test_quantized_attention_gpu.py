@@ -312,6 +312,24 @@ def test_quantized_attention_window_below_residual(W, L, device):
     assert max_abs(o, ref) < ATTN_TOL
 
 
+@pytest.mark.parametrize("G", [1, 12, 16])
+@pytest.mark.parametrize("W", [32, 64])
+def test_quantized_attention_window_below_residual_groups(G, W, device):
+    """W < R (1-2 residual tiles, the sink the only quantized group) with
+    query groups of 1, 12 and 16 heads: each output correctly rounded."""
+    from quant_kernel import build_quantized_kv_cache
+    B, KVH, D = 3, 2, 128
+    H = G * KVH
+    kc = randn((B, KVH, S + W, D), 60 + W + G, np.float16)
+    vc = randn((B, KVH, S + W, D), 61 + W + G, np.float16)
+    q16 = randn((B, H, D), 62 + W + G, np.float16)
+    say(f"kivi W={W} < R, G={G}")
+    cache = build_quantized_kv_cache(dev(kc, device), dev(vc, device))
+    o = _attend(dev(q16, device), cache, 163840, W)
+    ref = O.quantized_attention_masked(q16, _host_cache(cache), 163840, W, SCALE)
+    assert_nearly_rounded(o, ref)
+
+
 def test_quantized_attention_rejects_small_window(device):
     from quant_kernel import build_quantized_kv_cache
     kc = torch.zeros(1, 2, S + 256, 128, dtype=torch.float16, device=device)

@@ -87,6 +87,30 @@ def test_sparse_steady_state_windows(W, device):
     assert max_abs(o, o_ring) < 1e-3
 
 
+@pytest.mark.parametrize("G", [1, 4, 12, 16])
+@pytest.mark.parametrize("W", [60, 256, 1024])
+def test_sparse_query_group_sizes(G, W, device):
+    """Query groups of 1..16 heads through both fp16 kernels (W <= 476: the
+    single-pass lean kernel with interleaved tiles; W=1024: the work-queue
+    kernel), steady state and ramp-up, each output correctly rounded."""
+    from helpers import assert_nearly_rounded
+    B, KVH, D = 3, 2, 128
+    H = G * KVH
+    for L in (S + W // 2, 100000):
+        q16 = randn((B, H, D), 31 + G + L, np.float16)
+        kf = randn((B, KVH, min(L, S + W + 8), D), 32 + W, np.float16)
+        vf = randn((B, KVH, min(L, S + W + 8), D), 33 + W, np.float16)
+        n = min(L, S + W)
+        kc = np.zeros((B, KVH, S + W, D), np.float16)
+        vc = np.zeros((B, KVH, S + W, D), np.float16)
+        kc[:, :, :n] = kf[:, :, :n]
+        vc[:, :, :n] = vf[:, :, :n]
+        say(f"sparse G={G} W={W} L={L}")
+        o = _run(q16, kc, vc, L, W, device)
+        ref = O.sparse_attention_compacted(q16, kc, vc, L, W, S, SCALE)
+        assert_nearly_rounded(o, ref)
+
+
 def test_sparse_rejects_bad_cache_shape(device):
     from sparse_kernel import sparse_decode_attention
     q = torch.zeros(2, 64, 128, dtype=torch.float16, device=device)
