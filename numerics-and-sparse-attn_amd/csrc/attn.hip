@@ -120,7 +120,8 @@ struct QRef {
 // sink + 32 i ..), item nwt is the sink group (`sink` real tokens at slots
 // 0..sink-1; the cheapest tile, so it comes last in the queue).  MIXED: the
 // wave also holds fp16-tile accumulators (and steps no fp16 tile after).
-template <bool MIXED>
+// PACK: the packed layout (query groups of at most kPackGroup heads).
+template <bool MIXED, bool PACK>
 struct QItems {
   typedef QTileRaw Raw;
   typedef QRef State;
@@ -139,8 +140,8 @@ struct QItems {
   }
   __device__ __forceinline__ void step(int i, const Raw& X, State& s, const StepCtx& c) const {
     const bool sk = i == n - 1;
-    q_tile_step<MIXED>(X, c.slot, c.qB, sk ? 0 : sink + kTile * i, sk ? sink : kTile, c.R,
-                       c.scale_log2, s.st, s.qs, c.lane);
+    q_tile_step<MIXED, PACK>(X, c.slot, c.qB, sk ? 0 : sink + kTile * i, sk ? sink : kTile, c.R,
+                             c.scale_log2, s.st, s.qs, c.lane);
   }
 };
 
@@ -228,9 +229,12 @@ __device__ __forceinline__ void publish_f(const AttnCommon& P, const WaveState& 
 // pair goes out as one 8-byte write.  All 16 head rows are written (rows of heads >= G stay inside the
 // wave's slot and the merge never reads them), so no write is predicated.
 // ADD: the slot already holds this wave's fp16-tile rows (all reads are
-// issued before any write, so the adds wait on LDS once).
-template <bool ADD>
+// issued before any write, so the adds wait on LDS once).  PACK: the
+// remainder rows are folded in first (rows 8..15 then repeat heads 0..7),
+// or, with FOLD false, published as rows 8..15 for the merge to add.
+template <bool ADD, bool PACK = false, bool FOLD = true>
 __device__ __forceinline__ void publish_q(QState& qs, char* slot, int lane) {
+  if (PACK && FOLD) q_state_fold(qs);
   const int t = lane & 15, g = lane >> 4;
   float2v v[4][4];
   uint32_t off[4][4];
@@ -525,8 +529,9 @@ struct KiviStepArgs<kSeqStep> {
   StreamArgs a;
 };
 
-template <int MODE>
+template <int MODE, bool PACK>
 struct KiviSrcBase : KiviStepArgs<MODE> {
+  static constexpr bool kPackQ = PACK;   // Q operand in the packed layout
   const _Float16* kres;
   const _Float16* vres;
   int res_rows;
@@ -625,12 +630,12 @@ struct KiviSrcBase : KiviStepArgs<MODE> {
       Wq.vs += (size_t)pair * win_tok * 4;
       Wq.vz += (size_t)pair * win_tok * 4;
     }
-    QItems<true> qit;   // tiles of a wave that also holds fp16-tile accumulators
+    QItems<true, PACK> qit;   // tiles of a wave that also holds fp16-tile accumulators
     qit.sinkq = S;
     qit.winq = Wq;
     qit.n = 1 + nwt;
     qit.sink = sink;
-    QItems<false> qonly;
+    QItems<false, PACK> qonly;
     qonly.sinkq = S;
     qonly.winq = Wq;
     qonly.n = 1 + nwt;
@@ -669,7 +674,7 @@ struct KiviSrcBase : KiviStepArgs<MODE> {
         if constexpr (MODE != kOneRange) c.R = R;
         qonly.step(nqw + rw, E, qref, c);
         publish_ml(P, st, c.lds, lane, wave);
-        publish_q<false>(qs, c.slot, lane);
+        publish_q<false, PACK>(qs, c.slot, lane);
         return;
       }
       if (hand) {
@@ -725,7 +730,7 @@ struct KiviSrcBase : KiviStepArgs<MODE> {
         const int s0 = grab(ctr + 1, lane);
         const int s1 = grab(ctr + 1, lane);
         if (s0 < qit.n) {
-          Ring<QItems<true>> qring;
+          Ring<QItems<true, PACK>> qring;
           ring_begin(qit, qring, s0, s1, lane);
           ring_run_dynamic(qit, qring, ctr + 1, qref, c);
           has_q = true;
@@ -733,14 +738,14 @@ struct KiviSrcBase : KiviStepArgs<MODE> {
       }
       publish_ml(P, st, c.lds, lane, wave);
       publish_f(P, st, c.slot, lane);
-      if (has_q) publish_q<true>(qs, c.slot, lane);
+      if (has_q) publish_q<true, PACK>(qs, c.slot, lane);
     } else {
       // Both entries are loaded even when the second is past the queue:
       // those loads return nothing but hold the quantized waves a little
       // longer before the barrier, which keeps the residual tiles' loads
       // behind every quantized tile's (measured: skipping them costs about
       // 0.5 us per step at window 256..288).
-      Ring<QItems<false>> qring;
+      Ring<QItems<false, PACK>> qring;
       ring_begin(qonly, qring, qw, qw + nqw + nrw, lane);
       sync(c, dyn || nqw > 0);
       if constexpr (MODE != kOneRange) c.R = R;
@@ -749,17 +754,31 @@ struct KiviSrcBase : KiviStepArgs<MODE> {
       else
         ring_run_static(qonly, qring, qref, c);
       publish_ml(P, st, c.lds, lane, wave);
-      publish_q<false>(qs, c.slot, lane);
+      publish_q<false, PACK>(qs, c.slot, lane);
     }
   }
 };
 
-struct KiviSrc : KiviSrcBase<kOneRange> {};
-struct KiviVarSrc : KiviSrcBase<kSeqLens> {};
-struct KiviRingSrc : KiviSrcBase<kSeqRings> {};
+template <bool PACK>
+struct KiviSrc : KiviSrcBase<kOneRange, PACK> {};
+template <bool PACK>
+struct KiviVarSrc : KiviSrcBase<kSeqLens, PACK> {};
+template <bool PACK>
+struct KiviRingSrc : KiviSrcBase<kSeqRings, PACK> {};
 // The decode-time cache with one ring state per sequence, stepped by one
 // token in the same launch (kvdec_kivi_stream_step_decode).
-struct KiviStepSrc : KiviSrcBase<kSeqStep> {};
+template <bool PACK>
+struct KiviStepSrc : KiviSrcBase<kSeqStep, PACK> {};
+
+// Whether a source's kernel takes the Q operand in the packed layout.
+template <class Src, class = void>
+struct packs_q {
+  static constexpr bool value = false;
+};
+template <class Src>
+struct packs_q<Src, decltype((void)Src::kPackQ)> {
+  static constexpr bool value = Src::kPackQ;
+};
 
 template <class Src>
 __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) {
@@ -787,9 +806,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) 
   // into MFMA B-operand order (lane (n, g): head n, channels 32c + 8g .. +7)
   // before any tile load, so no wave waits on another to start computing.
   // Lanes of heads >= G read past the resource: zeros, no memory access.
+  // In the packed layout lanes n and n + 8 both take head n & 7.
   half8 qB[4];
   {
-    const int n = lane & 15, g = lane >> 4;
+    const int n = packs_q<Src>::value ? lane & 7 : lane & 15, g = lane >> 4;
     const rsrc_t rq = make_rsrc(P.q + ((size_t)b * P.H + (size_t)kvh * P.G) * kHeadDim,
                                 (uint32_t)P.G * kRowBytes);
     const uint32_t qoff = n < P.G ? (uint32_t)n * kRowBytes + 16u * (uint32_t)g : kOOB;
@@ -844,7 +864,7 @@ struct LeanCommon {
 // The first part of every lean kernel: kernel-argument lines fetched in one
 // scalar-cache round trip, then the Q operand of this KV head's G query
 // heads in MFMA B-operand order (heads >= G read zeros without an access).
-template <class Args>
+template <class Args, bool PACK = false>
 __device__ __forceinline__ void lean_prologue(const LeanCommon& C, uint32_t head, int lane, half8 (&qB)[4]) {
   {
     constexpr int kArgLines = (int)(sizeof(Args) + 63) / 64;
@@ -855,7 +875,7 @@ __device__ __forceinline__ void lean_prologue(const LeanCommon& C, uint32_t head
     for (int i = 0; i < 4; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
     asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]));
   }
-  const int n = lane & 15, g = lane >> 4;
+  const int n = PACK ? lane & 7 : lane & 15, g = lane >> 4;   // PACK: lanes n, n + 8 take head n & 7
   const rsrc_t rq = make_rsrc(C.q + (size_t)head * C.G * kHeadDim, (uint32_t)C.G * kRowBytes);
   const uint32_t qoff = n < C.G ? (uint32_t)n * kRowBytes + 16u * (uint32_t)g : kOOB;
 #pragma unroll
@@ -864,7 +884,10 @@ __device__ __forceinline__ void lean_prologue(const LeanCommon& C, uint32_t head
 }
 
 // Barrier, then one thread per (head, 4 channels) combines the 8 waves'
-// published partials into the fp16 output rows of this KV head.
+// published partials into the fp16 output rows of this KV head.  Waves
+// below NPACK published packed quantized rows unfolded: their row hn + 8
+// (the remainder part) is added to row hn.
+template <int NPACK = 0>
 __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds, uint32_t head) {
   __syncthreads();
   const float* sh_m = reinterpret_cast<const float*>(lds + kLdsM);
@@ -880,6 +903,12 @@ __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds,
     lw[w] = sh_l[w * kMaxGroup + hn];
     ow[w] = *reinterpret_cast<const float4v*>(lds + kLdsSlots + w * kSlotBytes + row_off(hn, ch));
   }
+  float4v orem[NPACK > 0 ? NPACK : 1];
+#pragma unroll
+  for (int w = 0; w < NPACK; ++w)
+    orem[w] = *reinterpret_cast<const float4v*>(lds + kLdsSlots + w * kSlotBytes + row_off(hn + 8, ch));
+#pragma unroll
+  for (int w = 0; w < NPACK; ++w) ow[w] += orem[w];
   float M = mw[0];
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) M = fmaxf(M, mw[w]);
@@ -991,13 +1020,14 @@ struct KiviLeanArgs {
   int sink;
 };
 
+template <bool PACK>
 __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) {
   extern __shared__ __align__(16) char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t head = blockIdx.x;
   half8 qB[4];
-  lean_prologue<KiviLeanArgs>(A.c, head, lane, qB);
+  lean_prologue<KiviLeanArgs, PACK>(A.c, head, lane, qB);
   char* slot = lds + kLdsSlots + wave * kSlotBytes;
   const int nwt = A.nwt;
   WaveState st;
@@ -1019,13 +1049,13 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     __syncthreads();
     auto step = [&](int i, const QTileRaw& X) {
       const bool sk = i == nwt;
-      q_tile_step<false>(X, slot, qB, sk ? 0 : A.sink + kTile * i, sk ? A.sink : kTile, A.c.R,
-                         A.c.scale_log2, st, qs, lane);
+      q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * i, sk ? A.sink : kTile, A.c.R,
+                               A.c.scale_log2, st, qs, lane);
     };
     if (wave < n_q) step(wave, X0);
     if (wave + 4 < n_q) step(wave + 4, X1);
     lean_publish_ml(A.c.G, st, lds, lane, wave);
-    publish_q<false>(qs, slot, lane);
+    publish_q<false, PACK, false>(qs, slot, lane);
   } else {
     // residual tile w - 4: rows 32 (w - 4) .. + 31 (interleaving the four
     // tiles' rows, or issuing V after the softmax, measured slower here:
@@ -1047,7 +1077,7 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     lean_publish_ml(A.c.G, st, lds, lane, wave);
     lean_publish_f(A.c.G, st, slot, lane);
   }
-  lean_merge(A.c, lds, head);
+  lean_merge<PACK ? 4 : 0>(A.c, lds, head);   // PACK: waves 0..3 left their rows unfolded
 }
 
 // Streaming read of `n16` 16-byte words, for the measurement of a decode
@@ -1242,7 +1272,8 @@ int check_dense(const void* q, const void* k, const void* v, void* o, int dtype,
   return KVDEC_OK;
 }
 
-int kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
+template <bool PACK>
+int kivi_decode_t(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
                 void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH, int64_t seq_len,
                 int32_t window, int32_t sink, int32_t residual, int32_t group, int32_t bits,
                 float sm_scale, void* stream) {
@@ -1282,7 +1313,7 @@ int kivi_decode(const void* q, const void* k_res, const void* v_res, const void*
 
   auto u8 = [&](int i) { return static_cast<const uint8_t*>(kivi[i]); };
   auto f16 = [&](int i) { return static_cast<const _Float16*>(kivi[i]); };
-  KiviVarSrc S{};
+  KiviVarSrc<PACK> S{};
   S.kres = static_cast<const _Float16*>(k_res);
   S.vres = static_cast<const _Float16*>(v_res);
   S.res_rows = res_rows;
@@ -1316,10 +1347,10 @@ int kivi_decode(const void* q, const void* k_res, const void* v_res, const void*
     A.sink_meta_bytes = (uint32_t)(P.pairs * 256);
     A.nwt = S.nwt;
     A.sink = sink;
-    hipLaunchKernelGGL(kivi_lean_kernel, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, st, A);
+    hipLaunchKernelGGL(kivi_lean_kernel<PACK>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, st, A);
     return launch_status();
   }
-  KiviSrc S1{};
+  KiviSrc<PACK> S1{};
   S1.kres = S.kres;
   S1.vres = S.vres;
   S1.res_rows = S.res_rows;
@@ -1331,9 +1362,35 @@ int kivi_decode(const void* q, const void* k_res, const void* v_res, const void*
   return launch_attn(P, S1, true, 0, st);
 }
 
+// Query groups of at most kPackGroup heads take the packed-layout kernels
+// from kPackMinGroups window-old groups on.  The packed step issues fewer
+// instructions but has longer dependency chains; it pays once waves step
+// more than one quantized tile (the lean kernel's four quantized waves take
+// a second tile from 4 window-old groups on).  Measured per step: W = 160,
+// 5.58 -> 5.73 us packed; W = 256, 6.38 -> 6.17 us.
+constexpr int kPackMinGroups = 4;
+bool packed_group(int32_t H, int32_t KVH, int64_t window_old_groups) {
+  return window_old_groups >= kPackMinGroups && KVH > 0 && H % KVH == 0 && H / KVH <= kPackGroup;
+}
+
+int kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
+                void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH, int64_t seq_len,
+                int32_t window, int32_t sink, int32_t residual, int32_t group, int32_t bits,
+                float sm_scale, void* stream) {
+  const int64_t res_rows = window < residual ? window : residual;
+  if (packed_group(H, KVH, group > 0 ? (window - res_rows) / group : 0))
+    return kivi_decode_t<true>(
+      q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window, sink, residual, group, bits,
+      sm_scale, stream);
+  return kivi_decode_t<false>(
+      q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window, sink, residual, group, bits,
+      sm_scale, stream);
+}
+
 // The fused decode over a decode-time KIVI cache: one ring state for every
 // sequence (ring null: ring_start / ring_count) or one per sequence.
-int stream_decode(const void* q, const void* k_ring, const void* v_ring, const void* const* kivi,
+template <bool PACK>
+int stream_decode_t(const void* q, const void* k_ring, const void* v_ring, const void* const* kivi,
                   void* o, const int32_t* ring, int64_t B, int32_t H, int32_t KVH, int32_t sink,
                   int32_t n_groups, int32_t ring_cap, int32_t ring_start, int32_t ring_count,
                   int32_t group, int32_t bits, float sm_scale, void* stream) {
@@ -1374,7 +1431,7 @@ int stream_decode(const void* q, const void* k_ring, const void* v_ring, const v
 
   auto u8 = [&](int i) { return static_cast<const uint8_t*>(kivi[i]); };
   auto f16 = [&](int i) { return static_cast<const _Float16*>(kivi[i]); };
-  KiviRingSrc S{};
+  KiviRingSrc<PACK> S{};
   S.kres = static_cast<const _Float16*>(k_ring);
   S.vres = static_cast<const _Float16*>(v_ring);
   S.res_rows = ring_cap;
@@ -1386,7 +1443,7 @@ int stream_decode(const void* q, const void* k_ring, const void* v_ring, const v
   S.lens = ring;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (ring) return launch_attn(P, S, true, 0, st);
-  KiviSrc S1{};
+  KiviSrc<PACK> S1{};
   S1.kres = S.kres;
   S1.vres = S.vres;
   S1.res_rows = S.res_rows;
@@ -1398,9 +1455,23 @@ int stream_decode(const void* q, const void* k_ring, const void* v_ring, const v
   return launch_attn(P, S1, true, 0, st);
 }
 
+int stream_decode(const void* q, const void* k_ring, const void* v_ring, const void* const* kivi,
+                  void* o, const int32_t* ring, int64_t B, int32_t H, int32_t KVH, int32_t sink,
+                  int32_t n_groups, int32_t ring_cap, int32_t ring_start, int32_t ring_count,
+                  int32_t group, int32_t bits, float sm_scale, void* stream) {
+  if (packed_group(H, KVH, n_groups))
+    return stream_decode_t<true>(
+      q, k_ring, v_ring, kivi, o, ring, B, H, KVH, sink, n_groups, ring_cap, ring_start,
+      ring_count, group, bits, sm_scale, stream);
+  return stream_decode_t<false>(
+      q, k_ring, v_ring, kivi, o, ring, B, H, KVH, sink, n_groups, ring_cap, ring_start,
+      ring_count, group, bits, sm_scale, stream);
+}
+
 // One token step of the per-sequence decode-time cache and the decode over
 // the stepped state, in one launch.
-int stream_step_decode(const void* q, const void* k_new, const void* v_new, void* k_ring, void* v_ring,
+template <bool PACK>
+int stream_step_decode_t(const void* q, const void* k_new, const void* v_new, void* k_ring, void* v_ring,
                        void* const* kivi, void* o, int32_t* appended, const int32_t* active,
                        int32_t* arrive, int32_t* plan, int32_t* ring, int64_t B, int32_t H,
                        int32_t KVH, int32_t sink, int32_t residual, int32_t n_groups,
@@ -1436,7 +1507,7 @@ int stream_step_decode(const void* q, const void* k_new, const void* v_new, void
 
   auto u8 = [&](int i) { return static_cast<uint8_t*>(kivi[i]); };
   auto f16 = [&](int i) { return static_cast<_Float16*>(kivi[i]); };
-  KiviStepSrc S{};
+  KiviStepSrc<PACK> S{};
   S.kres = static_cast<const _Float16*>(k_ring);
   S.vres = static_cast<const _Float16*>(v_ring);
   S.res_rows = ring_cap;
@@ -1469,6 +1540,20 @@ int stream_step_decode(const void* q, const void* k_new, const void* v_new, void
   a.KVH = KVH;
   a.residual = residual;
   return launch_attn(P, S, true, 0, static_cast<hipStream_t>(stream));
+}
+
+int stream_step_decode(const void* q, const void* k_new, const void* v_new, void* k_ring, void* v_ring,
+                       void* const* kivi, void* o, int32_t* appended, const int32_t* active,
+                       int32_t* arrive, int32_t* plan, int32_t* ring, int64_t B, int32_t H,
+                       int32_t KVH, int32_t sink, int32_t residual, int32_t n_groups,
+                       int32_t ring_cap, int32_t group, int32_t bits, float sm_scale, void* stream) {
+  if (packed_group(H, KVH, n_groups))
+    return stream_step_decode_t<true>(
+      q, k_new, v_new, k_ring, v_ring, kivi, o, appended, active, arrive, plan, ring, B, H, KVH,
+      sink, residual, n_groups, ring_cap, group, bits, sm_scale, stream);
+  return stream_step_decode_t<false>(
+      q, k_new, v_new, k_ring, v_ring, kivi, o, appended, active, arrive, plan, ring, B, H, KVH,
+      sink, residual, n_groups, ring_cap, group, bits, sm_scale, stream);
 }
 
 }  // namespace

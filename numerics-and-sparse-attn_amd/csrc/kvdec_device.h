@@ -105,6 +105,20 @@ __device__ __forceinline__ float4v mfma16x16x32(u32x4 a, half8 b, float4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(a), b, c, 0, 0, 0);
 }
 
+// Packed KIVI layout, for query groups of at most kPackGroup heads: the MFMA
+// columns (QK) and rows (PV) 8..15, padding otherwise, carry the fp16
+// remainder half of each two-part operand, so one MFMA does the work of a
+// head-and-remainder pair; lanes n and n + 8 of a row of 16 hold the same
+// head n & 7.  pack_lanes is all ones in the lanes n >= 8.
+constexpr int kPackGroup = 8;
+__device__ __forceinline__ uint32_t pack_lanes(int lane) { return (lane & 8) ? ~0u : 0u; }
+
+// x plus the x of lane n ^ 8 of the same row of 16 lanes (DPP row_ror:8).
+__device__ __forceinline__ float add_half_row(float x) {
+  const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false);
+  return x + __builtin_bit_cast(float, y);
+}
+
 // Token (0..31) of a tile held in slot j (0..7) by lane group g: the C-layout
 // of two stacked 16x16 QK blocks, reused as the PV reduction order.
 __device__ __forceinline__ int tau(int g, int j) { return 16 * (j >> 2) + 4 * g + (j & 3); }
@@ -545,6 +559,22 @@ __device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lan
   for (int b = 0; b < 8; ++b) qs.O[b] = qs.O[b] * ar;
 }
 
+// Packed layout: rows 8..15 of each accumulator hold the remainder parts of
+// heads 0..7; add them to rows 0..7 (lanes L and L ^ 32), leaving the sums in
+// both halves.  The exchange goes through ds_bpermute: this toolchain (ROCm
+// 7.2 clang) miscompiles v_permlane32_swap applied to the elements of a
+// vector (the elements after the first are replaced by the first's result).
+__device__ __forceinline__ void q_state_fold(QState& qs) {
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const float4v x = qs.O[b];
+    float4v y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = __shfl_xor(x[r], 32);
+    qs.O[b] = x + y;
+  }
+}
+
 // Layout of a staged KIVI tile inside a wave slot (bytes):
 //   [0, 1024)     K codes, 8 byte rows x 128 channels (as stored)
 //   [1024, 1280)  K scales [128], [1280, 1536) negated K zeros [128]
@@ -583,6 +613,8 @@ __device__ __forceinline__ u32x2 lds_read_tr8(const char* p) {
 // fp16(a0 * b.lo - c.lo) in the low half and fp16(a1 * b.hi - c.hi) in the
 // high half of the result, from the fp32 a0, a1 and the fp16 pairs b, c:
 // v_fma_mixlo_f16 then v_fma_mixhi_f16 (each writes its half of the dword).
+// The compiler's own form of this (two v_fma_mix_f32 and a
+// v_cvt_pk_f16_f32, rounding twice) measured no faster in the kernels.
 __device__ __forceinline__ uint32_t fma_mix_pk_f16(float a0, float a1, uint32_t b, uint32_t c) {
   uint32_t d;
   asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,1,1]" : "=v"(d) : "v"(a0), "v"(b), "v"(c));
@@ -629,11 +661,25 @@ __device__ __forceinline__ u32x2 fields2(u32x2 w, uint32_t sh) {
 // PV.  Masked tokens get p = 0; their codes are finite.
 constexpr float kSlackVScale = 128.0f;
 
-template <bool MIXED, bool HALF>
+// PACK (query groups of at most kPackGroup heads): QK's B operand holds the
+// fp16 product q * scale in columns 0..7 and its exact remainder in columns
+// 8..15, so one MFMA per block covers both and lanes n, n + 8 add their
+// logits (zero term included); PV's A operand holds P' rounded to fp16 in
+// rows 0..7 and the remainder in rows 8..15, which the accumulators keep
+// apart until q_state_fold.  The remainder is fp16(pr * scale + e), where
+// pB + pr is p (pr = fp16(p - pB)) and e = pB * scale - fp16(pB * scale) is
+// exact: ~2^-21 of P' instead of ~2^-22.  Lanes of both halves take each
+// operand from one instruction sequence: the lane mask zeroes the
+// subtrahend below row 8 and the remainder term's factor.  Subtrahends are
+// negated as bits with the mask (one v_bitop3 per dword), not as fp16: the
+// compiler turns some fp16 negations of packed operands into three-step
+// integer sequences.
+template <bool MIXED, bool HALF, bool PACK>
 __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[4], int slot0,
                                             int xlim, const SlotRanges& R, float scale_log2,
                                             float slack, WaveState& st, QState& qs, int lane) {
   const int t = lane & 15, g = lane >> 4;
+  const uint32_t pm = PACK ? pack_lanes(lane) : 0u;
   // scale and negated zero of the lane's K channels 32c + 8g .. +7
   half8 ks[4], nz[4];
 #pragma unroll
@@ -650,9 +696,12 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const half8 qh = qB[c] * ks[c];
-    const half8 ql = __builtin_elementwise_fma(qB[c], ks[c], -qh);
-    sz = mfma16x16x32(as_u4(nz[c]), qh, sz);
-    sz = mfma16x16x32(as_u4(nz[c]), ql, sz);
+    // PACK: qh in columns 0..7, the remainder q * scale - qh in 8..15
+    const half8 qx =
+        PACK ? __builtin_elementwise_fma(qB[c], ks[c], as_h8((as_u4(qh) ^ kNegPk) & pm)) : qh;
+    const half8 ql = PACK ? qx : __builtin_elementwise_fma(qB[c], ks[c], -qh);
+    sz = mfma16x16x32(as_u4(nz[c]), qx, sz);
+    if (!PACK) sz = mfma16x16x32(as_u4(nz[c]), ql, sz);
 #pragma unroll
     for (int blk = 0; blk < (HALF ? 1 : 2); ++blk) {
       const u32x2 w =
@@ -660,19 +709,18 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
       const u32x2 f = fields2(w, sh);
       const u32x2 d0 = codes_f16(f[0], kCodeScale), d1 = codes_f16(f[1], kCodeScale);
       const u32x4 d = {d0[0], d0[1], d1[0], d1[1]};
-      if (blk == 0) {
-        s0 = mfma16x16x32(d, qh, s0);
-        s0 = mfma16x16x32(d, ql, s0);
-      } else {
-        s1 = mfma16x16x32(d, qh, s1);
-        s1 = mfma16x16x32(d, ql, s1);
-      }
+      float4v& sb = blk == 0 ? s0 : s1;
+      sb = mfma16x16x32(d, qx, sb);
+      if (!PACK) sb = mfma16x16x32(d, ql, sb);
     }
   }
   const float xz = sz[0] * scale_log2;
   float x[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) x[j] = fmaf(j < 4 ? s0[j & 3] : s1[j & 3], scale_log2, xz);
+  for (int j = 0; j < 8; ++j) {
+    x[j] = fmaf(j < 4 ? s0[j & 3] : s1[j & 3], scale_log2, xz);
+    if (PACK) x[j] = add_half_row(x[j]);
+  }
   if (!(xlim == kTile && tile_fully_valid(R, slot0))) {
     const uint32_t valid = tile_valid_bits(R, slot0, xlim, lane);
 #pragma unroll
@@ -702,6 +750,16 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
     pB[j] = (_Float16)pf[j];
   }
   st.l += ls;
+  // PACK: the lane-masked -pB and pr = fp16(p - pB) (zero in rows 0..7)
+  u32x4 nBm = {0u, 0u, 0u, 0u}, prm = {0u, 0u, 0u, 0u};
+  if (PACK) {
+    const u32x4 pBu = as_u4(pB);
+    constexpr uint32_t kOnePk = 0x3C003C00u;   // fp16 pair (1, 1)
+    const u32x4 pr = {fma_mix_pk_f16(pf[0], pf[1], kOnePk, pBu[0]), fma_mix_pk_f16(pf[2], pf[3], kOnePk, pBu[1]),
+                      fma_mix_pk_f16(pf[4], pf[5], kOnePk, pBu[2]), fma_mix_pk_f16(pf[6], pf[7], kOnePk, pBu[3])};
+    nBm = (pBu ^ kNegPk) & pm;
+    prm = pr & pm;
+  }
 
   // PV, one V group (32 channels, code byte columns 8 grp .. 8 grp + 7) at
   // a time.  One transposed LDS read gives lane (t, g) byte column
@@ -722,11 +780,19 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
     const u32x2 z_hi = *reinterpret_cast<const u32x2*>(slot + kQsVZ + grp * 64 + 32 + 8 * g);
     const u32x2 vb = lds_read_tr8(vrow + 8 * grp);
     const u32x4 vsc = {s_lo[0], s_lo[1], s_hi[0], s_hi[1]};
-    // head: fp16 product of the fp16 p and scale; remainder: p * scale -
-    // head, rounded once (one mixed-precision fused multiply-add per value)
-    const u32x4 pq = as_u4(pB * as_h8(vsc));
-    const u32x4 pl = {fma_mix_pk_f16(pf[0], pf[1], vsc[0], pq[0]), fma_mix_pk_f16(pf[2], pf[3], vsc[1], pq[1]),
-                      fma_mix_pk_f16(pf[4], pf[5], vsc[2], pq[2]), fma_mix_pk_f16(pf[6], pf[7], vsc[3], pq[3])};
+    u32x4 pq, pl;
+    if (PACK) {
+      const half8 hn = as_h8(nBm) * as_h8(vsc);                          // rows >= 8: -fp16(pB s)
+      const half8 e = __builtin_elementwise_fma(pB, as_h8(vsc), hn);     // rows < 8: fp16(pB s)
+      pq = as_u4(__builtin_elementwise_fma(as_h8(prm), as_h8(vsc), e));  // rows >= 8: pr s + e
+      pl = pq;
+    } else {
+      // head: fp16 product of the fp16 p and scale; remainder: p * scale -
+      // head, rounded once (one mixed-precision fused multiply-add per value)
+      pq = as_u4(pB * as_h8(vsc));
+      pl = u32x4{fma_mix_pk_f16(pf[0], pf[1], vsc[0], pq[0]), fma_mix_pk_f16(pf[2], pf[3], vsc[1], pq[1]),
+                 fma_mix_pk_f16(pf[4], pf[5], vsc[2], pq[2]), fma_mix_pk_f16(pf[6], pf[7], vsc[3], pq[3])};
+    }
     const half8 nzv = as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]});
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
@@ -737,14 +803,14 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
       const half8 b = as_h8(u32x4{b0[0], b0[1], b1[0], b1[1]});
       float4v& acc = qs.O[2 * grp + m];
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pq), b, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), b, acc, 0, 0, 0);
+      if (!PACK) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), b, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pq), nzv, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), nzv, acc, 0, 0, 0);
+      if (!PACK) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pl), nzv, acc, 0, 0, 0);
     }
   }
 }
 
-template <bool MIXED>
+template <bool MIXED, bool PACK = false>
 __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
                                             const half8 (&qB)[4], int slot0, int xlim,
                                             const SlotRanges& R, float scale_log2, WaveState& st,
@@ -755,9 +821,9 @@ __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
   const float slack =
       __ballot(!(fmaxf((float)vs[0], (float)vs[1]) <= kSlackVScale)) ? 0.0f : kRescaleSlack;
   if (xlim <= kTile / 2)
-    q_tile_body<MIXED, true>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+    q_tile_body<MIXED, true, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
   else
-    q_tile_body<MIXED, false>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+    q_tile_body<MIXED, false, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
 }
 
 }  // namespace kvdec
