@@ -1043,17 +1043,23 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
                             : q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
       load_q_group(T, sk ? head : head * (uint32_t)nwt + (uint32_t)i, i < n_q, lane, X);
     };
+    // A wave whose second item is the sink group loads and steps it first:
+    // its few bytes arrive early, and the wave's last step is no longer the
+    // sink's next to a residual wave's step on the same SIMD (W=256: 0.5 to
+    // 1.8% faster over three A/B runs).
+    const bool sink_first = wave + 4 == nwt;
+    const int i0 = sink_first ? wave + 4 : wave, i1 = sink_first ? wave : wave + 4;
     QTileRaw X0, X1;
-    load(wave, X0);
-    load(wave + 4, X1);
+    load(i0, X0);
+    load(i1, X1);
     __syncthreads();
     auto step = [&](int i, const QTileRaw& X) {
       const bool sk = i == nwt;
       q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * i, sk ? A.sink : kTile, A.c.R,
                                A.c.scale_log2, st, qs, lane);
     };
-    if (wave < n_q) step(wave, X0);
-    if (wave + 4 < n_q) step(wave + 4, X1);
+    if (i0 < n_q) step(i0, X0);
+    if (i1 < n_q) step(i1, X1);
     lean_publish_ml(A.c.G, st, lds, lane, wave);
     publish_q<false, PACK, false>(qs, slot, lane);
   } else {
