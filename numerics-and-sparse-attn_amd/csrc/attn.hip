@@ -1086,6 +1086,158 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
   lean_merge<PACK ? 4 : 0>(A.c, lds, head);   // PACK: waves 0..3 left their rows unfolded
 }
 
+// The fused KIVI decode past the lean kernel's windows (more than 7
+// window-old groups), for query groups of at most kPackGroup heads (the
+// packed layout) and a residual of at most 128 rows: 16 waves, four per
+// SIMD, so that the VALU the quantized steps saturate always has another
+// wave's instructions to issue (a tile-step microbenchmark: 2043 cycles
+// per tile per SIMD at 4 waves per SIMD and one tile in flight per wave,
+// 2270 at 2 waves and two in flight; 128 VGPRs leave room for one).  Waves
+// 0..11 start on window-old groups 0..11, waves 12..15 on residual tiles
+// 0..3; the rest of the quantized items (window-old groups, then the sink
+// group) are claimed from an LDS counter, the claim and the next item's
+// loads issued before the current item's step.  A residual wave publishes
+// its fp16 partial to its own area before it joins the quantized queue, so
+// the merge combines 20 partials.
+// Below 12 window-old groups every quantized wave steps at most one group
+// and the 8-wave kernel is faster (measured per step, W = 384 / 480 / 512:
+// 8.11 / 8.96 / 9.89 us there, 8.45 / 9.42 / 9.22 us here).
+constexpr int kWideMinGroups = 12;
+constexpr int kWideWaves = 16;
+constexpr int kWideThreads = 64 * kWideWaves;
+constexpr int kWideQWaves = 12;                  // waves that start on quantized items
+constexpr int kWideParts = kWideWaves + 4;       // + the residual waves' fp16 partials
+constexpr int kWideLdsCtr = 0;
+constexpr int kWideLdsM = 16;
+constexpr int kWideLdsL = kWideLdsM + kWideParts * kMaxGroup * 4;
+constexpr int kWideLdsSlots = (kWideLdsL + kWideParts * kMaxGroup * 4 + 255) & ~255;
+constexpr int kWideF16Bytes = kPackGroup * kHeadDim * 4;   // an fp16 partial of <= 8 heads
+constexpr int kWideLdsF16 = kWideLdsSlots + kWideWaves * kSlotBytes;
+constexpr int kWideLdsBytes = kWideLdsF16 + 4 * kWideF16Bytes;
+static_assert(kWideLdsBytes <= 160 * 1024, "wide kernel LDS");
+
+__device__ __forceinline__ void wide_publish_ml(int G, WaveState& st, char* lds, int lane, int part) {
+  st.l = group_sum(st.l);
+  const int n = lane & 15, g = lane >> 4;
+  if (n < G && g == 0) {
+    reinterpret_cast<float*>(lds + kWideLdsM)[part * kMaxGroup + n] = st.m;
+    reinterpret_cast<float*>(lds + kWideLdsL)[part * kMaxGroup + n] = st.l;
+  }
+}
+
+template <bool PACK>
+__global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs A) {
+  extern __shared__ __align__(16) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t head = blockIdx.x;
+  half8 qB[4];
+  lean_prologue<KiviLeanArgs, PACK>(A.c, head, lane, qB);
+  char* slot = lds + kWideLdsSlots + wave * kSlotBytes;
+  int* ctr = reinterpret_cast<int*>(lds + kWideLdsCtr);
+  const int nwt = A.nwt, n_q = nwt + 1;
+  const QTensors Tw = q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
+  const QTensors Ts = q_tensors(A.sinkq, A.sink_code_bytes, A.sink_meta_bytes);
+  // item i < nwt: window-old group i; item nwt: the sink group
+  auto load = [&](int i, QTileRaw& X) {
+    const bool sk = i == nwt;
+    load_q_group(sk ? Ts : Tw, sk ? head : head * (uint32_t)nwt + (uint32_t)i, i < n_q, lane, X);
+  };
+  if (threadIdx.x == 0) *ctr = kWideQWaves;
+  QTileRaw X;
+  int i = n_q;
+  if (wave < kWideQWaves) {
+    i = wave;
+    load(i, X);
+  }
+  __syncthreads();
+  if (wave >= kWideQWaves) {
+    // residual tile r: rows 32 r .. + 31; rows past res_rows are slots past
+    // the window (masked, V read as zeros)
+    const int r = wave - kWideQWaves;
+    const int slot0 = A.sink + kTile * nwt + kTile * r;
+    const rsrc_t rk = make_rsrc(A.kres, A.res_bytes), rv = make_rsrc(A.vres, A.res_bytes);
+    const uint32_t soff = head * (uint32_t)(A.res_rows * kRowBytes);
+    const bool has = r * kTile < A.res_rows;
+    const uint32_t base = has && tile_any_valid(A.c.R, slot0) ? (uint32_t)r * kSlotBytes : kOOB;
+    WaveState sf;
+    wave_state_init(sf);
+    if (has) {
+      F16Raw F;
+      load_f16(rk, rv, base, soff, lane, F);
+      f16_tile_step(F, slot, qB, slot0, A.c.R, A.c.scale_log2, sf, lane);
+    }
+    wide_publish_ml(A.c.G, sf, lds, lane, kWideWaves + r);
+    lean_publish_f(A.c.G, sf, lds + kWideLdsF16 + r * kWideF16Bytes, lane);
+    i = grab(ctr, lane);
+    load(i, X);
+  }
+  WaveState st;   // the quantized items' max and sum (st.O stays zero)
+  wave_state_init(st);
+  QState qs;
+  q_state_init(qs);
+  // window-old groups; the sink group (claimed last, at most 16 tokens: the
+  // host's condition) is stepped after the loop, so that the loop holds one
+  // tile body (with two, the registers of 4 waves per SIMD do not suffice)
+  while (i < nwt) {
+    const float slack = q_tile_stage(X, slot, lane);
+    const int nx = grab(ctr, lane);
+    load(nx, X);
+    q_tile_body<false, false, PACK>(slot, qB, A.sink + kTile * i, kTile, A.c.R, A.c.scale_log2, slack, st, qs,
+                                    lane);
+    i = nx;
+  }
+  if (i == nwt) {
+    const float slack = q_tile_stage(X, slot, lane);
+    q_tile_body<false, true, PACK>(slot, qB, 0, A.sink, A.c.R, A.c.scale_log2, slack, st, qs, lane);
+  }
+  wide_publish_ml(A.c.G, st, lds, lane, wave);
+  publish_q<false, PACK, false>(qs, slot, lane);
+
+  // merge: one thread per (head, 4 channels) over the 16 quantized partials
+  // (rows hn + 8 hold the packed remainder parts) and the 4 fp16 partials
+  __syncthreads();
+  const int e = threadIdx.x;
+  if (e >= A.c.G * 32) return;
+  const float* sh_m = reinterpret_cast<const float*>(lds + kWideLdsM);
+  const float* sh_l = reinterpret_cast<const float*>(lds + kWideLdsL);
+  const int hn = e >> 5, ch = e & 31;
+  float mw[kWideParts];
+#pragma unroll
+  for (int p = 0; p < kWideParts; ++p) mw[p] = sh_m[p * kMaxGroup + hn];
+  float M = mw[0];
+#pragma unroll
+  for (int p = 1; p < kWideParts; ++p) M = fmaxf(M, mw[p]);
+  float L = 0.f;
+  float4v acc = {0.f, 0.f, 0.f, 0.f};
+  // four partials at a time (their reads issued together)
+#pragma unroll
+  for (int p0 = 0; p0 < kWideParts; p0 += 4) {
+    float lw[4];
+    float4v ow[4], orem[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j;
+      lw[j] = sh_l[p * kMaxGroup + hn];
+      const char* part = p < kWideWaves ? lds + kWideLdsSlots + p * kSlotBytes
+                                        : lds + kWideLdsF16 + (p - kWideWaves) * kWideF16Bytes;
+      ow[j] = *reinterpret_cast<const float4v*>(part + row_off(hn, ch));
+      if (PACK && p < kWideWaves) orem[j] = *reinterpret_cast<const float4v*>(part + row_off(hn + 8, ch));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = p0 + j;
+      const float f = __builtin_amdgcn_exp2f(mw[p] - M);
+      L += lw[j] * f;
+      acc += (PACK && p < kWideWaves ? ow[j] + orem[j] : ow[j]) * f;
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
+              (_Float16)(acc[3] * inv)};
+  *reinterpret_cast<half4v*>(A.c.o + ((size_t)head * A.c.G + hn) * kHeadDim + 4 * ch) = h;
+}
+
 // Streaming read of `n16` 16-byte words, for the measurement of a decode
 // step's floor at the same launch scale (a workgroup reads one contiguous
 // share, 512 threads x 4 loads in flight, non-temporal as the decode's
@@ -1338,7 +1490,13 @@ int kivi_decode_t(const void* q, const void* k_res, const void* v_res, const voi
   // the lean kernel: at most 4 residual tiles, at most 7 window-old groups,
   // and every tensor small enough for 31-bit offsets
   const int64_t lean_bytes = P.pairs * (int64_t)res_rows * kRowBytes;
-  if (res_rows <= 4 * kTile && S.nwt + 1 <= 2 * 4 && lean_bytes < ((int64_t)1 << 31)) {
+  const bool lean = S.nwt + 1 <= 2 * 4;
+  // the wide kernel: packed query groups, at least kWideMinGroups
+  // window-old groups, a sink of at most 16 tokens, and the window-old code
+  // tensors small enough for 31-bit offsets too
+  const bool wide = PACK && S.nwt >= kWideMinGroups && P.G <= kPackGroup && sink <= kTile / 2 &&
+                    P.pairs * (int64_t)S.nwt * 1024 < ((int64_t)1 << 31);
+  if (res_rows <= 4 * kTile && (lean || wide) && lean_bytes < ((int64_t)1 << 31)) {
     KiviLeanArgs A;
     A.c = lean_common(P);
     A.kres = S.kres;
@@ -1353,7 +1511,10 @@ int kivi_decode_t(const void* q, const void* k_res, const void* v_res, const voi
     A.sink_meta_bytes = (uint32_t)(P.pairs * 256);
     A.nwt = S.nwt;
     A.sink = sink;
-    hipLaunchKernelGGL(kivi_lean_kernel<PACK>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, st, A);
+    if (lean)
+      hipLaunchKernelGGL(kivi_lean_kernel<PACK>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, st, A);
+    else if constexpr (PACK)
+      hipLaunchKernelGGL(kivi_wide_kernel<true>, dim3((unsigned)P.pairs), dim3(kWideThreads), kWideLdsBytes, st, A);
     return launch_status();
   }
   KiviSrc<PACK> S1{};

@@ -810,20 +810,33 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   }
 }
 
+// Stage a loaded tile into the wave's slot and return its rescale slack;
+// the registers of `raw` are free afterwards.
+__device__ __forceinline__ float q_tile_stage(const QTileRaw& raw, char* slot, int lane) {
+  stage_q_raw(raw, slot, lane);
+  // every lane holds two of the tile's 128 V scales
+  const half2v vs = __builtin_bit_cast(half2v, raw.vs);
+  return __ballot(!(fmaxf((float)vs[0], (float)vs[1]) <= kSlackVScale)) ? 0.0f : kRescaleSlack;
+}
+
+// Consume the staged tile (xlim real tokens: the sink group has at most 16).
+template <bool MIXED, bool PACK = false>
+__device__ __forceinline__ void q_tile_consume(char* slot, const half8 (&qB)[4], int slot0, int xlim,
+                                               const SlotRanges& R, float scale_log2, float slack,
+                                               WaveState& st, QState& qs, int lane) {
+  if (xlim <= kTile / 2)
+    q_tile_body<MIXED, true, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+  else
+    q_tile_body<MIXED, false, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+}
+
 template <bool MIXED, bool PACK = false>
 __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
                                             const half8 (&qB)[4], int slot0, int xlim,
                                             const SlotRanges& R, float scale_log2, WaveState& st,
                                             QState& qs, int lane) {
-  stage_q_raw(raw, slot, lane);
-  // every lane holds two of the tile's 128 V scales
-  const half2v vs = __builtin_bit_cast(half2v, raw.vs);
-  const float slack =
-      __ballot(!(fmaxf((float)vs[0], (float)vs[1]) <= kSlackVScale)) ? 0.0f : kRescaleSlack;
-  if (xlim <= kTile / 2)
-    q_tile_body<MIXED, true, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
-  else
-    q_tile_body<MIXED, false, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+  const float slack = q_tile_stage(raw, slot, lane);
+  q_tile_consume<MIXED, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
 }
 
 }  // namespace kvdec

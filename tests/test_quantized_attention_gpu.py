@@ -238,20 +238,22 @@ def test_quantized_attention_dominant_token(where, device):
     assert_nearly_rounded(o, ref)
 
 
-@pytest.mark.parametrize("L", [1, 3, 4, 5, 60, 200, 300, 387, 388, 389])
-def test_quantized_attention_rampup(L, device):
+@pytest.mark.parametrize("W,L", [(384, L) for L in (1, 3, 4, 5, 60, 200, 300, 387, 388, 389)] +
+                         [(1024, L) for L in (3, 500, 900, 1027, 1028, 1029)])
+def test_quantized_attention_rampup(W, L, device):
     """Ramp-up (seq_len <= S + W): only the slots the _kv_indices rule marks
     valid are attended.  Unwritten slots hold 3.0 before quantization: far
     enough from N(0,1) data that a leak moves the output, small enough that
     the quantization groups they share with real tokens stay well conditioned
-    (1e4, as in the fp16 sparse test, would swamp those groups' scales)."""
+    (1e4, as in the fp16 sparse test, would swamp those groups' scales).
+    W = 384 runs the 8-wave kernel, W = 1024 the 16-wave one."""
     from quant_kernel import build_quantized_kv_cache
-    B, H, KVH, D, W = 2, 16, 2, 128, 384
+    B, H, KVH, D = 2, 16, 2, 128
     kf = randn((B, KVH, max(L, 1), D), 30 + L)
     vf = randn((B, KVH, max(L, 1), D), 31 + L)
     kc, vc = O.build_compacted_cache(kf, vf, L, W, S, garbage=3.0)
     q16 = randn((B, H, D), 32 + L, np.float16)
-    say(f"kivi ramp L={L}")
+    say(f"kivi ramp W={W} L={L}")
     cache = build_quantized_kv_cache(dev(kc.astype(np.float16), device), dev(vc.astype(np.float16), device))
     o = _attend(dev(q16, device), cache, L, W)
     ref = O.quantized_attention_masked(q16, _host_cache(cache), L, W, SCALE)
