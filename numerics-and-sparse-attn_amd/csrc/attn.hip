@@ -862,25 +862,78 @@ struct LeanCommon {
 };
 
 // The first part of every lean kernel: kernel-argument lines fetched in one
-// scalar-cache round trip, then the Q operand of this KV head's G query
-// heads in MFMA B-operand order (heads >= G read zeros without an access).
+// scalar-cache round trip (lean_kernargs), then (lean_prologue) the Q
+// operand of this KV head's G query heads in MFMA B-operand order (heads
+// >= G read zeros without an access).
+template <class Args>
+__device__ __forceinline__ void lean_kernargs() {
+  constexpr int kArgLines = (int)(sizeof(Args) + 63) / 64;
+  static_assert(kArgLines <= 4, "kernel arguments span more lines than are touched");
+  const cint32* ka = (const cint32*)__builtin_amdgcn_kernarg_segment_ptr();
+  int32_t x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
+  asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]));
+}
+
 template <class Args, bool PACK = false>
 __device__ __forceinline__ void lean_prologue(const LeanCommon& C, uint32_t head, int lane, half8 (&qB)[4]) {
-  {
-    constexpr int kArgLines = (int)(sizeof(Args) + 63) / 64;
-    static_assert(kArgLines <= 4, "kernel arguments span more lines than are touched");
-    const cint32* ka = (const cint32*)__builtin_amdgcn_kernarg_segment_ptr();
-    int32_t x[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
-    asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]));
-  }
+  lean_kernargs<Args>();
   const int n = PACK ? lane & 7 : lane & 15, g = lane >> 4;   // PACK: lanes n, n + 8 take head n & 7
   const rsrc_t rq = make_rsrc(C.q + (size_t)head * C.G * kHeadDim, (uint32_t)C.G * kRowBytes);
   const uint32_t qoff = n < C.G ? (uint32_t)n * kRowBytes + 16u * (uint32_t)g : kOOB;
 #pragma unroll
   for (int cc = 0; cc < 4; ++cc)
     qB[cc] = as_h8(__builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 64u * cc, 0, 0));
+}
+
+// Q through LDS.  Instead of every wave loading its whole B operand (four
+// 1 KiB load instructions per wave, all issued ahead of the tile loads, and
+// a CU issues its loads one instruction at a time), quarter w of the KV
+// head's 16 query rows (rows 4w .. 4w + 3, zeros past G) is loaded by wave
+// w with one 1 KiB instruction and stored into the Q area once it has
+// arrived; every wave reads its operand from there once the four quarters
+// are in (KIVI W=256 6.08 -> 5.83 us, W=128 5.57 -> 5.24).  Rows are 272
+// bytes apart, so that the operand reads (16 rows at one column) spread
+// over the LDS banks.  A workgroup barrier instead of the readiness count
+// measured slower (7.07 us at W=256): the waves that issue the residual
+// tiles' loads reach it only once the memory pipeline has taken them all.
+// The sparse fp16 kernel takes the same path (W=256 7.85 -> 7.55 us); the
+// 16-wave KIVI kernel does not (W=1024 / 4096 0.6-0.8% slower with it).
+constexpr int kQPitch = kRowBytes + 16;
+constexpr int kQAreaBytes = kMaxGroup * kQPitch;
+constexpr int kQLdsBytes = kQAreaBytes + 16;   // + the readiness count
+__device__ __forceinline__ u32x4 q_quarter_load(const LeanCommon& C, uint32_t head, int quarter, int lane) {
+  const rsrc_t rq = make_rsrc(C.q + (size_t)head * C.G * kHeadDim, (uint32_t)C.G * kRowBytes);
+  return bload16(rq, (uint32_t)(quarter * 4 * kRowBytes + 16 * lane));
+}
+__device__ __forceinline__ void q_quarter_store(char* qarea, int quarter, int lane, u32x4 v) {
+  *reinterpret_cast<u32x4*>(qarea + (4 * quarter + (lane >> 4)) * kQPitch + 16 * (lane & 15)) = v;
+}
+// The Q area's readiness count (quarters stored), in the word after it:
+// zeroed before a workgroup barrier that precedes every increment,
+// incremented (release, one lane) by each wave that stored its quarter,
+// polled (acquire) before the operand is read.  The poll is bounded (~10^7
+// cycles; the four storing waves run unconditionally, so it ends long
+// before that).
+__device__ __forceinline__ void q_quarter_ready(char* qarea, int lane) {
+  if (lane == 0)
+    __hip_atomic_fetch_add(reinterpret_cast<int*>(qarea + kQAreaBytes), 1, __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void q_area_wait(const char* qarea) {
+  for (int it = 0; it < (1 << 16); ++it) {
+    if (__hip_atomic_load(reinterpret_cast<const int*>(qarea + kQAreaBytes), __ATOMIC_ACQUIRE,
+                          __HIP_MEMORY_SCOPE_WORKGROUP) >= 4)
+      break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+template <bool PACK>
+__device__ __forceinline__ void q_operand_read(const char* qarea, int lane, half8 (&qB)[4]) {
+  const int n = PACK ? lane & 7 : lane & 15, g = lane >> 4;   // PACK: lanes n, n + 8 take head n & 7
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) qB[cc] = *reinterpret_cast<const half8*>(qarea + n * kQPitch + 64 * cc + 16 * g);
 }
 
 // Barrier, then one thread per (head, 4 channels) combines the 8 waves'
@@ -955,8 +1008,27 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t head = blockIdx.x;
+  lean_kernargs<F16LeanArgs>();
+  // Q through LDS (waves 0..3 load a quarter each, the readiness count
+  // zeroed before a barrier that precedes every increment)
+  char* qarea = lds + kLdsBytes;
+  if (threadIdx.x == 0) *reinterpret_cast<int*>(qarea + kQAreaBytes) = 0;
+  __syncthreads();
+  u32x4 qv = {0u, 0u, 0u, 0u};
+  if (wave < 4) qv = q_quarter_load(A.c, head, wave, lane);
   half8 qB[4];
-  lean_prologue<F16LeanArgs>(A.c, head, lane, qB);
+  // after the wave's first loads: its quarter stored, then the operand read
+  // once all four are in (the store waits only for the quarter)
+  auto q_in = [&](bool read) {
+    if (wave < 4) {
+      q_quarter_store(qarea, wave, lane, qv);
+      q_quarter_ready(qarea, lane);
+    }
+    if (read) {
+      q_area_wait(qarea);
+      q_operand_read<false>(qarea, lane, qB);
+    }
+  };
   char* slot = lds + kLdsSlots + wave * kSlotBytes;
   const size_t off = (size_t)head * A.rows * kHeadDim;
   const uint32_t bytes = (uint32_t)A.rows * kRowBytes;
@@ -976,6 +1048,7 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
     F16Raw X0, X1;
     load_f16(rk, rv, rows(wave), live(wave), 0u, lane, X0);
     load_f16(rk, rv, rows(wave + kWaves), live(wave + kWaves), 0u, lane, X1);
+    q_in(true);
     f16_tile_step(X0, slot, qB, rows(wave), A.c.R, A.c.scale_log2, st, lane);
     f16_tile_step(X1, slot, qB, rows(wave + kWaves), A.c.R, A.c.scale_log2, st, lane);
   } else if (wave < n_tiles) {
@@ -985,10 +1058,13 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
     const TileRows T = rows(wave);
     const bool lv = live(wave);
     load_f16_k(rk, T, lv, 0u, lane, X);
+    q_in(true);
     uint32_t valid;
     const TileProbs P = f16_tile_probs(X, slot, qB, T, A.c.R, A.c.scale_log2, st, lane, valid);
     load_f16_v(rv, T, after_probs(lv, P), 0u, lane, X);
     f16_tile_pv(X, P, valid, st);
+  } else {
+    q_in(false);   // no tile, but waves 0..3 still provide their quarter
   }
   lean_publish_ml(A.c.G, st, lds, lane, wave);
   lean_publish_f(A.c.G, st, slot, lane);
@@ -1026,13 +1102,17 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t head = blockIdx.x;
+  lean_kernargs<KiviLeanArgs>();
+  char* qarea = lds + kLdsBytes;
   half8 qB[4];
-  lean_prologue<KiviLeanArgs, PACK>(A.c, head, lane, qB);
   char* slot = lds + kLdsSlots + wave * kSlotBytes;
   const int nwt = A.nwt;
   WaveState st;
   wave_state_init(st);
   if (wave < 4) {
+    // Q quarter w first, then the groups' loads: the wait for the quarter
+    // (after the barrier, before its store) leaves them in flight
+    const u32x4 qv = q_quarter_load(A.c, head, wave, lane);
     QState qs;
     q_state_init(qs);
     const int n_q = nwt + 1;
@@ -1053,6 +1133,10 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     load(i0, X0);
     load(i1, X1);
     __syncthreads();
+    q_quarter_store(qarea, wave, lane, qv);
+    q_quarter_ready(qarea, lane);
+    q_area_wait(qarea);
+    q_operand_read<PACK>(qarea, lane, qB);
     auto step = [&](int i, const QTileRaw& X) {
       const bool sk = i == nwt;
       q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * i, sk ? A.sink : kTile, A.c.R,
@@ -1075,11 +1159,12 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     const bool has = tile * kTile < A.res_rows;
     const uint32_t base = has && tile_any_valid(A.c.R, slot0) ? (uint32_t)tile * kSlotBytes : kOOB;
     F16Raw X;
+    if (wave == 4 && lane == 0) *reinterpret_cast<int*>(qarea + kQAreaBytes) = 0;
     __syncthreads();
-    if (has) {
-      load_f16(rk, rv, base, soff, lane, X);
-      f16_tile_step(X, slot, qB, slot0, A.c.R, A.c.scale_log2, st, lane);
-    }
+    if (has) load_f16(rk, rv, base, soff, lane, X);
+    q_area_wait(qarea);
+    q_operand_read<PACK>(qarea, lane, qB);
+    if (has) f16_tile_step(X, slot, qB, slot0, A.c.R, A.c.scale_log2, st, lane);
     lean_publish_ml(A.c.G, st, lds, lane, wave);
     lean_publish_f(A.c.G, st, slot, lane);
   }
@@ -1390,7 +1475,7 @@ int launch_f16_lean(const AttnCommon& P, const _Float16* k, const _Float16* v, i
   A.k = k;
   A.v = v;
   A.rows = rows;
-  hipLaunchKernelGGL(f16_lean_kernel, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, stream, A);
+  hipLaunchKernelGGL(f16_lean_kernel, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes + kQLdsBytes, stream, A);
   return launch_status();
 }
 
@@ -1512,7 +1597,7 @@ int kivi_decode_t(const void* q, const void* k_res, const void* v_res, const voi
     A.nwt = S.nwt;
     A.sink = sink;
     if (lean)
-      hipLaunchKernelGGL(kivi_lean_kernel<PACK>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes, st, A);
+      hipLaunchKernelGGL(kivi_lean_kernel<PACK>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes + kQLdsBytes, st, A);
     else if constexpr (PACK)
       hipLaunchKernelGGL(kivi_wide_kernel<true>, dim3((unsigned)P.pairs), dim3(kWideThreads), kWideLdsBytes, st, A);
     return launch_status();
