@@ -899,7 +899,9 @@ __device__ __forceinline__ void lean_prologue(const LeanCommon& C, uint32_t head
 // measured slower (7.07 us at W=256): the waves that issue the residual
 // tiles' loads reach it only once the memory pipeline has taken them all.
 // The sparse fp16 kernel takes the same path (W=256 7.85 -> 7.55 us); the
-// 16-wave KIVI kernel does not (W=1024 / 4096 0.6-0.8% slower with it).
+// 16-wave KIVI kernel does not (W=1024 / 4096 0.6-0.8% slower with it), nor
+// does attn_kernel (through its `sync`: the decode-time cache's W=256 step
+// 7.14 -> 7.36 us, W=384 8.41 -> 8.64).
 constexpr int kQPitch = kRowBytes + 16;
 constexpr int kQAreaBytes = kMaxGroup * kQPitch;
 constexpr int kQLdsBytes = kQAreaBytes + 16;   // + the readiness count
