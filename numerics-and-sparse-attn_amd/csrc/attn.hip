@@ -847,10 +847,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) 
 // share is at most two tiles, one workgroup of 8 waves per KV head runs a
 // fixed program per wave: the KV head is the workgroup index (no division:
 // query row b * H + kvh * G of the head is head * G), every per-head address
-// is one multiply by a host-computed stride, and each wave issues its Q
-// operand and all of its tile loads before it waits on anything (no work
-// queue, no barrier before the merge).  The tile steps, the published
-// partials and the LDS merge are those of attn_kernel.
+// is one multiply by a host-computed stride, and each wave issues all of
+// its tile loads before it waits on anything (no work queue; Q comes
+// through LDS, see q_quarter_load).  The tile steps, the published partials
+// and the LDS merge are those of attn_kernel.  (The 16-wave KIVI kernel
+// shares the prologue and the tile steps, with a work queue.)
 // ---------------------------------------------------------------------------
 
 struct LeanCommon {
