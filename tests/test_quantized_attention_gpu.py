@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 S, R = 4, 128
 
 
-def _attend(q, cache, L, W, device=None):
+def _attend(q, cache, L, W, device=None, sink=S):
     from quant_kernel import sparse_decode_attention_quantized
     c = cache
     o = sparse_decode_attention_quantized(
@@ -24,7 +24,7 @@ def _attend(q, cache, L, W, device=None):
         c["v_sink_packed"], c["v_sink_scale"], c["v_sink_zero"],
         c["k_win_packed"], c["k_win_scale"], c["k_win_zero"],
         c["v_win_packed"], c["v_win_scale"], c["v_win_zero"],
-        seq_len=L, window=W)
+        seq_len=L, window=W, sink=sink)
     torch.cuda.synchronize()
     return host(o)
 
@@ -339,3 +339,27 @@ def test_quantized_attention_rejects_small_window(device):
     q = torch.zeros(1, 16, 128, dtype=torch.float16, device=device)
     with pytest.raises(ValueError):
         _attend(q, cache, 1000, 64)
+
+
+@pytest.mark.parametrize("sink", [1, 16, 17, 32])
+@pytest.mark.parametrize("W", [256, 1024])
+def test_quantized_attention_sink_sizes(sink, W, device):
+    """Sink groups of 1 to 32 real tokens (the API's sink argument): the
+    8-wave lean kernel (W=256), the 16-wave kernel (W=1024 with a sink of at
+    most 16 tokens: its half-group step after the loop) and the work-queue
+    kernel (W=1024, sink > 16), in steady state and ramp-up."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D = 2, 16, 2, 128
+    q16 = randn((B, H, D), 60 + sink + W, np.float16)
+    for L in (sink + W + 500, sink + W // 2):
+        kf = randn((B, KVH, L, D), 61 + sink + L)
+        vf = randn((B, KVH, L, D), 62 + sink + L)
+        kc, vc = O.build_compacted_cache(kf, vf, L, W, sink, garbage=3.0)
+        say(f"kivi sink={sink} W={W} L={L}")
+        cache = build_quantized_kv_cache(dev(kc.astype(np.float16), device), dev(vc.astype(np.float16), device),
+                                         sink=sink)
+        o = _attend(dev(q16, device), cache, L, W, sink=sink)
+        ref = O.quantized_attention_masked(q16, _host_cache(cache), L, W, SCALE, sink=sink)
+        assert max_abs(o, ref) < ATTN_TOL
+        if L > sink + W:
+            assert_nearly_rounded(o, ref)
