@@ -198,6 +198,14 @@ __device__ __forceinline__ uint32_t row_off(int head, int chunk) {
   return (uint32_t)head * 512u + 16u * (uint32_t)(chunk ^ head);
 }
 
+// The fp16 output of 4 channels, stored non-temporally (written once and
+// not read in this kernel: no L2 line is left dirty for the end-of-kernel
+// release; KIVI W=256 5.83 -> 5.79 us, W=32 4.24 -> 4.20, sparse W=256
+// 7.51 -> 7.48).
+__device__ __forceinline__ void store_out4(_Float16* p, half4v h) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x2, h), reinterpret_cast<u32x2*>(p));
+}
+
 __device__ __forceinline__ void publish_ml(const AttnCommon& P, WaveState& st, char* lds, int lane,
                                            int wave) {
   st.l = group_sum(st.l);
@@ -301,8 +309,7 @@ __device__ __forceinline__ void merge_out(const AttnCommon& P, char* lds, int64_
     const float inv = L > 0.f ? 1.0f / L : 0.f;   // L == 0: a sequence of length 0
     half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
                 (_Float16)(acc[3] * inv)};
-    *reinterpret_cast<half4v*>(P.o + ((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim +
-                               4 * ch) = h;
+    store_out4(P.o + ((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + 4 * ch, h);
   } else {
     const size_t idx = ((size_t)pair * P.n_splits + split) * P.G + hn;
     *reinterpret_cast<float4v*>(P.ws + idx * kHeadDim + 4 * ch) = acc;
@@ -979,7 +986,7 @@ __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds,
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
               (_Float16)(acc[3] * inv)};
-  *reinterpret_cast<half4v*>(C.o + ((size_t)head * C.G + hn) * kHeadDim + 4 * ch) = h;
+  store_out4(C.o + ((size_t)head * C.G + hn) * kHeadDim + 4 * ch, h);
 }
 
 __device__ __forceinline__ void lean_publish_ml(int G, WaveState& st, char* lds, int lane, int wave) {
@@ -1323,7 +1330,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
               (_Float16)(acc[3] * inv)};
-  *reinterpret_cast<half4v*>(A.c.o + ((size_t)head * A.c.G + hn) * kHeadDim + 4 * ch) = h;
+  store_out4(A.c.o + ((size_t)head * A.c.G + hn) * kHeadDim + 4 * ch, h);
 }
 
 // Streaming read of `n16` 16-byte words, for the measurement of a decode
@@ -1378,7 +1385,8 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnCommon P) {
     L += wl[idx] * f;
     acc += wo[idx * kHeadDim + d] * f;
   }
-  P.o[((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + d] = (_Float16)(L > 0.f ? acc / L : 0.f);
+  __builtin_nontemporal_store((_Float16)(L > 0.f ? acc / L : 0.f),
+                              P.o + ((size_t)b * P.H + (size_t)kvh * P.G + hn) * kHeadDim + d);
 }
 
 // ---------------------------------------------------------------------------
