@@ -931,19 +931,26 @@ __device__ __forceinline__ void q_quarter_ready(char* qarea, int lane) {
     __hip_atomic_fetch_add(reinterpret_cast<int*>(qarea + kQAreaBytes), 1, __ATOMIC_RELEASE,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ void q_area_wait(const char* qarea) {
-  for (int it = 0; it < (1 << 16); ++it) {
-    if (__hip_atomic_load(reinterpret_cast<const int*>(qarea + kQAreaBytes), __ATOMIC_ACQUIRE,
-                          __HIP_MEMORY_SCOPE_WORKGROUP) >= 4)
-      break;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
+// The operand read once the count is 4; should the bound ever run out, the
+// operand is NaN, so the outputs show it instead of using a partial Q.
 template <bool PACK>
 __device__ __forceinline__ void q_operand_read(const char* qarea, int lane, half8 (&qB)[4]) {
+  bool ready = false;
+  for (int it = 0; it < (1 << 16); ++it) {
+    if (__hip_atomic_load(reinterpret_cast<const int*>(qarea + kQAreaBytes), __ATOMIC_ACQUIRE,
+                          __HIP_MEMORY_SCOPE_WORKGROUP) >= 4) {
+      ready = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
   const int n = PACK ? lane & 7 : lane & 15, g = lane >> 4;   // PACK: lanes n, n + 8 take head n & 7
 #pragma unroll
   for (int cc = 0; cc < 4; ++cc) qB[cc] = *reinterpret_cast<const half8*>(qarea + n * kQPitch + 64 * cc + 16 * g);
+  if (!ready) {
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) qB[cc] = as_h8(u32x4{0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u});
+  }
 }
 
 // Barrier, then one thread per (head, 4 channels) combines the 8 waves'
@@ -1035,7 +1042,6 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
       q_quarter_ready(qarea, lane);
     }
     if (read) {
-      q_area_wait(qarea);
       q_operand_read<false>(qarea, lane, qB);
     }
   };
@@ -1145,7 +1151,6 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     __syncthreads();
     q_quarter_store(qarea, wave, lane, qv);
     q_quarter_ready(qarea, lane);
-    q_area_wait(qarea);
     q_operand_read<PACK>(qarea, lane, qB);
     auto step = [&](int i, const QTileRaw& X) {
       const bool sk = i == nwt;
@@ -1172,7 +1177,6 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     if (wave == 4 && lane == 0) *reinterpret_cast<int*>(qarea + kQAreaBytes) = 0;
     __syncthreads();
     if (has) load_f16(rk, rv, base, soff, lane, X);
-    q_area_wait(qarea);
     q_operand_read<PACK>(qarea, lane, qB);
     if (has) f16_tile_step(X, slot, qB, slot0, A.c.R, A.c.scale_log2, st, lane);
     lean_publish_ml(A.c.G, st, lds, lane, wave);
