@@ -82,18 +82,22 @@ def test_stream_matches_builder_after_evictions(W, device):
         assert max_abs(host(o), o_orc) < ATTN_TOL
 
 
-def test_stream_between_evictions_vs_oracle(device):
-    B, H, KVH, W = 2, 16, 2, 256
+# the ring decode's kernels: 8 heads per KV head with 4 and 7 window-old
+# groups (the lean kernel, packed), 16 heads (lean, unpacked), 8 window-old
+# groups (past the lean kernel)
+@pytest.mark.parametrize("H,KVH,W", [(16, 2, 256), (16, 2, 352), (32, 2, 256), (16, 2, 384)])
+def test_stream_between_evictions_vs_oracle(H, KVH, W, device):
+    B = 2
     L0 = S + W + 5
     steps = 70
-    cache, kf, vf, q = _stream(B, H, KVH, W, L0, steps, 77)
+    cache, kf, vf, q = _stream(B, H, KVH, W, L0, steps, 77 + W + H)
     kh, vh, qh = host(kf), host(vf), host(q)
     for step in range(steps):
         cache.append(kf[:, :, cache.seq_len], vf[:, :, cache.seq_len])
         if step % 9 != 4:
             continue
         L = cache.seq_len
-        say(f"stream between evictions L={L} count={cache.ring.count}")
+        say(f"stream between evictions H={H} KVH={KVH} W={W} L={L} count={cache.ring.count}")
         o = host(cache.attend(q))
         oc, wlen = O.stream_cache(kh, vh, L0, L, W)
         ref = O.quantized_attention(qh, wlen, oc, SCALE)
