@@ -558,6 +558,28 @@ struct KiviSrcBase : KiviStepArgs<MODE> {
   // residual makes every wave a residual wave with a dynamic residual queue,
   // and all quantized tiles dynamic.
   __device__ __forceinline__ int n_res() const { return (res_rows + kTile - 1) / kTile; }
+
+  // kSeqStep, after the decode: the last of the sequence's KVH workgroups
+  // to arrive records the step (every workgroup read the count at its
+  // start, before it arrives)
+  __device__ __forceinline__ void arrive(int64_t pair, const AttnCommon& P) const {
+    if constexpr (MODE == kSeqStep) {
+      const StreamArgs& a = this->a;
+      const int64_t b = pair / P.KVH;
+      if (threadIdx.x == kThreads - 1 && atomicAdd(a.arrive + b, 1) == P.KVH - 1) {
+        const int n = max((int)((cint32*)a.appended)[b], 0);
+        const bool act = !a.active || ((cint32*)a.active)[b] != 0;
+        const RingStep rs = ring_step(n, act, a.residual, a.cap, a.nwg);
+        a.arrive[b] = 0;
+        a.appended[b] = n + (act ? 1 : 0);
+        a.plan[3 * b] = rs.row;
+        a.plan[3 * b + 1] = rs.blk;
+        a.plan[3 * b + 2] = rs.blk >= 0 ? rs.slot : -1;
+        a.ring[2 * b] = rs.start;
+        a.ring[2 * b + 1] = rs.count;
+      }
+    }
+  }
   __device__ __forceinline__ int n_res_waves() const { return min(n_res(), kWaves); }
   __device__ __forceinline__ int n_static_q() const {
     const int nrw = n_res_waves(), nqw = kWaves - nrw;
@@ -591,33 +613,31 @@ struct KiviSrcBase : KiviStepArgs<MODE> {
       // anything: the token's K/V row written, the ring's oldest block
       // quantized into the oldest window-old slot when the ring fills, then
       // a workgroup barrier (the decode below reads both).  Every wave has
-      // the sequence's count before the barrier; after it, the last of the
-      // sequence's KVH workgroups to arrive records the step and advances
-      // the count (the writes reach the next launch at the kernel boundary).
+      // the sequence's count before the barrier; after the decode and its
+      // merge, the last of the sequence's KVH workgroups to arrive records
+      // the step and advances the count (arrive(), at the kernel's end: the
+      // arrival atomic's round trip no longer holds back the last wave's
+      // tile loads; the writes reach the next launch at the kernel
+      // boundary).
       const StreamArgs& a = this->a;
       const int64_t b = pair / P.KVH;
+      // the token's K/V row is loaded alongside the count (only the ring
+      // row it goes to depends on the count): one memory round trip less
+      // before the barrier
+      const bool row_thread = threadIdx.x < 2 * kRowBytes / 16;
+      const int i = threadIdx.x % (kRowBytes / 16);
+      const bool isv = threadIdx.x >= kRowBytes / 16;
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (row_thread)
+        x = *reinterpret_cast<const u32x4*>((isv ? a.v_new : a.k_new) + (size_t)pair * kHeadDim + 8 * i);
       const int n = max((int)((cint32*)a.appended)[b], 0);
       const bool act = !a.active || ((cint32*)a.active)[b] != 0;
       asm volatile("" ::"s"(n), "s"((int)act));   // both loaded before the barrier
       const RingStep rs = ring_step(n, act, a.residual, a.cap, a.nwg);
-      if (rs.row >= 0 && threadIdx.x < 2 * kRowBytes / 16) {
-        const int i = threadIdx.x % (kRowBytes / 16);
-        const bool isv = threadIdx.x >= kRowBytes / 16;
-        const u32x4 x = *reinterpret_cast<const u32x4*>((isv ? a.v_new : a.k_new) + (size_t)pair * kHeadDim + 8 * i);
+      if (rs.row >= 0 && row_thread)
         *reinterpret_cast<u32x4*>((isv ? a.v_ring : a.k_ring) + ((size_t)pair * a.cap + rs.row) * kHeadDim + 8 * i) = x;
-      }
       if (a.nwg > 0 && rs.blk >= 0) evict_block(a, pair, rs.blk, rs.slot, threadIdx.x, kThreads);
       __syncthreads();
-      // the workgroup's last thread (its wave writes no row and evicts less)
-      if (threadIdx.x == kThreads - 1 && atomicAdd(a.arrive + b, 1) == P.KVH - 1) {
-        a.arrive[b] = 0;
-        a.appended[b] = n + (act ? 1 : 0);
-        a.plan[3 * b] = rs.row;
-        a.plan[3 * b + 1] = rs.blk;
-        a.plan[3 * b + 2] = rs.blk >= 0 ? rs.slot : -1;
-        a.ring[2 * b] = rs.start;
-        a.ring[2 * b + 1] = rs.count;
-      }
       const int base = sink + win_tok, end = rs.start + rs.count;
       R = end <= res_rows ? SlotRanges{base, base + rs.start, base + end}
                           : SlotRanges{base + end - res_rows, base + rs.start, base + res_rows};
@@ -778,6 +798,13 @@ template <bool PACK>
 struct KiviStepSrc : KiviSrcBase<kSeqStep, PACK> {};
 
 // Whether a source's kernel takes the Q operand in the packed layout.
+// sources with an end-of-kernel hook (the KIVI sources: the decode-time
+// cache's step bookkeeping)
+template <class Src, class = void>
+struct has_arrive : std::false_type {};
+template <class Src>
+struct has_arrive<Src, decltype((void)&Src::arrive)> : std::true_type {};
+
 template <class Src, class = void>
 struct packs_q {
   static constexpr bool value = false;
@@ -847,6 +874,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) 
   wave_state_init(st);
   S.process(pair, split, P, wave, lane, ctr, sync, st);
   merge_out(P, lds, pair, split);
+  if constexpr (has_arrive<Src>::value) S.arrive(pair, P);
 }
 
 // ---------------------------------------------------------------------------
