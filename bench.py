@@ -153,28 +153,32 @@ def bytes_quantize(n_tok):
 # timing
 # --------------------------------------------------------------------------
 
-def graph_time(call, nsets, steps, warmup, min_steps=MIN_TIMED_STEPS, replays=None,
-               min_graph=MIN_GRAPH_STEPS):
-    """Per-step ms of back-to-back calls call(i % nsets), G = max(steps, nsets,
-    min_graph) of them captured in one HIP graph (every input set once per
-    pass), timed over R back-to-back replays (R * G >= min_steps unless
-    `replays` is given).  A replay carries a fixed cost (~20 us measured
-    between two back-to-back replays of one graph) that R * G steps share,
-    so G is kept long whatever `steps` is.  Returns (ms_per_step,
-    {"graph_steps": G, "replays": R})."""
-    G = max(steps, nsets, min_graph)
-    Rp = replays if replays is not None else max(2, math.ceil(min_steps / G))
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for i in range(min(3, G)):
-            call(i % nsets)
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
+CLOCK = {"lib": None}              # the timing build's ctypes handle under --kernel-clock
+CLOCK_LAUNCHES_PER_STEP = 2        # log slots per captured step (attention launches it may make)
+CLOCK_WGS = 1024                   # workgroup records per slot (kClockWgs in attn.hip)
+
+
+def _capture(body, G):
+    """Capture body() (which issues G steps) into one HIP graph; under
+    --kernel-clock the timing build's log is armed for the capture, so each
+    attention launch of the graph owns one slot.  Returns (graph, log)."""
+    lib = CLOCK["lib"]
+    log = None
+    if lib is not None:
+        log = torch.zeros(CLOCK_LAUNCHES_PER_STEP * G * CLOCK_WGS * 2, dtype=torch.int64, device="cuda")
+        if lib.kvdec_clock_arm(log.data_ptr(), CLOCK_LAUNCHES_PER_STEP * G) != 0:
+            raise RuntimeError("kvdec_clock_arm failed")
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(G):
-            call(i % nsets)
+    try:
+        with torch.cuda.graph(g):
+            out = body()
+    finally:
+        if lib is not None:
+            lib.kvdec_clock_arm(None, 0)
+    return g, log, out
+
+
+def _replay_time(g, G, Rp, warmup):
     for _ in range(max(1, warmup)):
         g.replay()
     torch.cuda.synchronize()
@@ -185,9 +189,124 @@ def graph_time(call, nsets, steps, warmup, min_steps=MIN_TIMED_STEPS, replays=No
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / (Rp * G)
+    return e0.elapsed_time(e1) / (Rp * G)
+
+
+def _clock_stats(g, log):
+    """One more replay with the log cleared: every workgroup of every
+    attention launch of the graph has stored the realtime counter at its
+    start and end.  Per launch: its own duration (last workgroup end - first
+    workgroup start), the gap to the next launch (its first start - this
+    launch's last end; negative = overlap), the dispatch ramp (last start -
+    first start) and the end spread (last end - first end), in us.  The
+    counter's rate is checked against HIP events around the same replay
+    (nominally 100 MHz)."""
+    log.zero_()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    a = log.cpu().numpy().view(np.uint64).reshape(-1, CLOCK_WGS, 2).astype(np.float64)
+    live = a[:, :, 0] > 0                                # workgroups that ran
+    keep = live.any(axis=1)
+    a, live = a[keep], live[keep]
+    if len(a) < 2:
+        return {"status": "no clocked launches recorded"}
+    big = np.where(live, a[:, :, 0], np.inf)
+    first = big.min(axis=1)
+    last_start = np.where(live, a[:, :, 0], -np.inf).max(axis=1)
+    first_end = np.where(live, a[:, :, 1], np.inf).min(axis=1)
+    last_end = np.where(live, a[:, :, 1], -np.inf).max(axis=1)
+    replay_us = e0.elapsed_time(e1) * 1e3
+    ticks = float(last_end[-1] - first[0])
+    rate = ticks / replay_us                             # ticks per us, the replay's fixed cost included
+    tick_us = 1.0 / 100.0 if abs(rate / 100.0 - 1.0) < 0.05 else 1.0 / rate
+    span = (last_end - first) * tick_us
+    gap = (first[1:] - last_end[:-1]) * tick_us
+    ramp = (last_start - first) * tick_us
+    tail = (last_end - first_end) * tick_us
+
+    def st(x):
+        return {"mean": round(float(np.mean(x)), 3), "median": round(float(np.median(x)), 3),
+                "min": round(float(np.min(x)), 3), "max": round(float(np.max(x)), 3)}
+    return {"launches": int(len(a)), "workgroups_per_launch": int(live.sum(axis=1).max()),
+            "counter_ticks_per_us_measured": round(rate, 2), "tick_us": tick_us,
+            "kernel_us": st(span), "gap_us": st(gap), "overlapping_launches": int((gap < 0).sum()),
+            "dispatch_ramp_us": st(ramp), "end_spread_us": st(tail),
+            "first_start_to_last_end_us_per_launch": round(ticks * tick_us / len(a), 3)}
+
+
+def graph_time(call, nsets, steps, warmup, min_steps=MIN_TIMED_STEPS, replays=None,
+               min_graph=MIN_GRAPH_STEPS):
+    """Per-step ms of back-to-back calls call(i % nsets), G = max(steps, nsets,
+    min_graph) of them captured in one HIP graph (every input set once per
+    pass), timed over R back-to-back replays (R * G >= min_steps unless
+    `replays` is given).  A replay carries a fixed cost (~20 us measured
+    between two back-to-back replays of one graph) that R * G steps share,
+    so G is kept long whatever `steps` is.  Returns (ms_per_step,
+    {"graph_steps": G, "replays": R}), plus "kernel_clock" under
+    --kernel-clock."""
+    G = max(steps, nsets, min_graph)
+    Rp = replays if replays is not None else max(2, math.ceil(min_steps / G))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(min(3, G)):
+            call(i % nsets)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    def body():
+        for i in range(G):
+            call(i % nsets)
+    g, log, _ = _capture(body, G)
+    ms = _replay_time(g, G, Rp, warmup)
+    info = {"graph_steps": G, "replays": Rp}
+    if log is not None:
+        info["kernel_clock"] = _clock_stats(g, log)
     del g
-    return ms, {"graph_steps": G, "replays": Rp}
+    return ms, info
+
+
+def chain_time(step, q0, nsets, steps, warmup, min_steps=MIN_TIMED_STEPS):
+    """The same timing for a dependent chain: step i attends with the query
+    q_i = o_{i-1} (q_0 = q0) over input set i % nsets, so no step can start
+    before the previous one has written its output, as in a decode loop
+    where each layer's attention waits for the last.  After the timing the
+    chain is rerun eagerly from q0 and its final output compared with the
+    graph's, bit for bit.  Returns (ms_per_step, info)."""
+    G = max(steps, nsets, MIN_GRAPH_STEPS)
+    Rp = max(2, math.ceil(min_steps / G))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        q = q0
+        for i in range(min(3, G)):
+            q = step(i % nsets, q)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    def body():
+        q = q0
+        for i in range(G):
+            q = step(i % nsets, q)
+        return q
+    g, log, q_graph = _capture(body, G)
+    ms = _replay_time(g, G, Rp, warmup)
+    info = {"graph_steps": G, "replays": Rp}
+    if log is not None:
+        info["kernel_clock"] = _clock_stats(g, log)
+    q = q0
+    for i in range(G):
+        q = step(i % nsets, q)
+    torch.cuda.synchronize()
+    info["final_output_equals_eager_chain"] = bool(torch.equal(q, q_graph))
+    info["final_output_max_abs_diff_vs_eager"] = float((q.float() - q_graph.float()).abs().max())
+    del g
+    return ms, info
 
 
 def latency_time(call, nsets, reps, flush):
@@ -362,6 +481,14 @@ def main():
                     help="windows of the 'sweep' path (fused KIVI decode, config 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-latency", action="store_true", help="skip the per-call latency runs")
+    ap.add_argument("--dense-lengths", default="163840,32768",
+                    help="context lengths of the 'dense' path (163840: the metric's L; 32768: config 2)")
+    ap.add_argument("--chain", choices=("both", "only", "off"), default="both",
+                    help="kivi and sparse paths: time the independent-input graph, the dependent chain "
+                         "(q <- o of the previous step), or both")
+    ap.add_argument("--kernel-clock", action="store_true",
+                    help="load the timing build (libkvdec_clock.so) and add each graph's per-launch kernel "
+                         "durations and launch gaps, read from the GPU realtime counter, to the paths")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first copy 256 MiB device-to-device three times: the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -372,9 +499,15 @@ def main():
               "build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
+    if args.kernel_clock:
+        os.environ["KVDEC_LIBRARY"] = "clock"
+    import _kvdec
     import dense_kernel
     import quant_kernel
     import sparse_kernel
+    if args.kernel_clock:
+        CLOCK["lib"] = _kvdec.lib
+    dense_lengths = [int(x) for x in args.dense_lengths.split(",") if x.strip()]
 
     paths = [p.strip() for p in args.paths.split(",") if p.strip()]
     K, Wu = max(1, args.steps), max(1, args.warmup)
@@ -424,18 +557,25 @@ def main():
             return quant_kernel.sparse_decode_attention_quantized(q, *a, seq_len=L, window=window)
         return call
 
-    def kivi_path(window, name, latency=True):
+    def kivi_path(window, name, latency=True, chain=False):
         ns, sets = kivi_sets(window)
         call = kivi_call(sets, window)
-        ms, ti = graph_time(call, ns, K, Wu)
-        lat = None if (flush is None or not latency) else latency_time(call, ns, 50, flush)
-        out[name] = path_record(ms, bytes_kivi(window), ns, ti, bytes_kivi(window, sink_tokens=32), lat)
-        progress(f"{name}: {out[name]['us_per_step']} us")
+        if not (chain and args.chain == "only"):
+            ms, ti = graph_time(call, ns, K, Wu)
+            lat = None if (flush is None or not latency) else latency_time(call, ns, 50, flush)
+            out[name] = path_record(ms, bytes_kivi(window), ns, ti, bytes_kivi(window, sink_tokens=32), lat)
+            progress(f"{name}: {out[name]['us_per_step']} us")
+        if chain and args.chain != "off":
+            def step(i, q):
+                return quant_kernel.sparse_decode_attention_quantized(q, *sets[i][1], seq_len=L, window=window)
+            ms, ti = chain_time(step, sets[0][0], ns, K, Wu)
+            out[name + "_chain"] = path_record(ms, bytes_kivi(window), ns, ti, bytes_kivi(window, sink_tokens=32))
+            progress(f"{name}_chain: {out[name + '_chain']['us_per_step']} us")
         return sets
 
     if "kivi" in paths:
-        sets = kivi_path(W, "kivi_w256")
-        if want_cpu:
+        sets = kivi_path(W, "kivi_w256", chain=True)
+        if want_cpu and "kivi_w256" in out:
             q0, parts = sets[0]
             us, reps = cpu_kivi(q0, dict(zip(KIVI_KEYS, parts)), W, budget_s=8.0)
             head_cpu = {"value": round(us, 1), "unit": "us/step", "cores": cpu["host"]["threads_used"],
@@ -510,20 +650,30 @@ def main():
             q, kc, vc = sets[i]
             return sparse_kernel.sparse_decode_attention(q, kc, vc, seq_len=L, window=W)
 
-        ms, ti = graph_time(call, ns, K, Wu)
-        lat = None if flush is None else latency_time(call, ns, 50, flush)
-        out["sparse_fp16_w256"] = path_record(ms, bytes_sparse(W), ns, ti, latency=lat)
-        if want_cpu:
+        if args.chain != "only":
+            ms, ti = graph_time(call, ns, K, Wu)
+            lat = None if flush is None else latency_time(call, ns, 50, flush)
+            out["sparse_fp16_w256"] = path_record(ms, bytes_sparse(W), ns, ti, latency=lat)
+
+        def sstep(i, q):
+            return sparse_kernel.sparse_decode_attention(q, sets[i][1], sets[i][2], seq_len=L, window=W)
+        if args.chain != "off":
+            ms, ti = chain_time(sstep, sets[0][0], ns, K, Wu)
+            out["sparse_fp16_w256_chain"] = path_record(ms, bytes_sparse(W), ns, ti)
+        if want_cpu and "sparse_fp16_w256" in out:
             us, reps = cpu_sparse(B, W)
             out["sparse_fp16_w256"]["cpu_us_per_step"] = round(us, 1)
-        progress(f"sparse_fp16_w256: {out['sparse_fp16_w256']['us_per_step']} us")
+        progress("sparse done: " + ", ".join(f"{k} {v['us_per_step']} us" for k, v in out.items()
+                                             if k.startswith("sparse")))
         del sets
 
     ms_warm = max(2, min(Wu, 3))
-    if "quantize" in paths or "dense" in paths or "paged" in paths:
-        k = randn(B, KVH, L, D)
-        k[..., outliers] *= 10
-        v = randn(B, KVH, L, D)
+    if "quantize" in paths or ("dense" in paths and dense_lengths) or "paged" in paths:
+        full = "quantize" in paths or "paged" in paths or ("dense" in paths and L in dense_lengths)
+        k = randn(B, KVH, L, D) if full else None
+        if full:
+            k[..., outliers] *= 10
+        v = randn(B, KVH, L, D) if full else None
         q = randn(B, H, D)
         if "quantize" in paths:
             ms, ti = graph_time(lambda i: quant_kernel.quantize_k_cache(k), 1, Kms, ms_warm, replays=2, min_graph=1)
@@ -531,7 +681,7 @@ def main():
             ms, ti = graph_time(lambda i: quant_kernel.quantize_v_cache(v), 1, Kms, ms_warm, replays=2, min_graph=1)
             out["quantize_v_L163840"] = path_record(ms, bytes_quantize(L), 1, ti)
             progress("quantize done")
-        if "dense" in paths:
+        if "dense" in paths and L in dense_lengths:
             ms, ti = graph_time(lambda i: dense_kernel.dense_decode_attention(q, k, v, seq_len=L), 1,
                                 Kms, ms_warm, replays=2, min_graph=1)
             out["dense_L163840"] = path_record(ms, bytes_dense(L), 1, ti)
@@ -562,7 +712,7 @@ def main():
             out["paged_nhd16_L163840"] = path_record(ms, bytes_paged(L, ps), 1, ti)
             del kp, vp, table, idx, lens
         del k, v
-        if "dense" in paths:
+        if "dense" in paths and 32768 in dense_lengths:
             # config 2: L = 32768 (a prefix view of the same cache would not be
             # contiguous, so the cache is regenerated at that length)
             Ls = 32768
@@ -625,37 +775,74 @@ def main():
 
     floor = None
     if "floor" in paths:
-        # what the box itself allows a decode step of each path: an empty
-        # launch of the decode grid, and a plain streaming read of the path's
-        # algorithmic bytes (kvdec_read_probe), timed like the paths
+        # what the box itself allows a decode step of each path: empty
+        # launches shaped like the decode kernels, and plain streaming reads
+        # of the path's algorithmic bytes (kvdec_read_probe_sweep), timed
+        # like the paths.  The headline's bytes get the whole sweep (grid x
+        # block size x load form); the other paths the sweep's best forms.
         import _kvdec as KV
-        sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+        sink = torch.zeros(65536, dtype=torch.int32, device=dev)
+        kinds = ("global_nt", "global", "buffer_nt", "buffer")
 
-        def probe_us(nbytes, blocks_list=(512, 1024)):
+        def cfg_name(blocks, threads, mode):
+            return f"{blocks}x{threads}/{kinds[mode & 3]}/{'upfront16' if mode & 4 else 'inflight4'}"
+
+        def probe_sets(nbytes):
             nb = (nbytes + 15) // 16 * 16
             ns = n_sets(nb) if nb else 1
-            bufs = [torch.empty(max(nb, 16) // 4, dtype=torch.int32, device=dev) for _ in range(ns)]
-            best = None
-            for blocks in blocks_list:
-                def pcall(i, blocks=blocks):
-                    KV.check(KV.lib.kvdec_read_probe(KV.ptr(bufs[i]), nb, KV.ptr(sink), blocks,
-                                                     KV.stream_of(sink)), "read_probe")
-                big = nb > (1 << 30)
-                ms, _ = (graph_time(pcall, ns, Kms, ms_warm, replays=2, min_graph=1) if big
-                         else graph_time(pcall, ns, K, Wu))
-                best = ms if best is None else min(best, ms)
-            del bufs
-            return round(best * 1e3, 3)
+            return nb, [torch.empty(max(nb, 16) // 4, dtype=torch.int32, device=dev) for _ in range(ns)]
 
-        floor = {"note": "per-step floors on this box: launch_us = an empty launch of the decode grid "
-                         "(256 workgroups x 512 threads) in the same graph timing; read_floor_us per path = "
-                         "kvdec_read_probe streaming the path's algorithmic bytes (best of 512 and 1024 "
-                         "workgroups); frac_of_read_floor = read_floor_us / us_per_step",
-                 "launch_us": probe_us(0, (256,))}
+        def probe_us(nb, bufs, blocks, threads, mode, lds=0):
+            def pcall(i):
+                KV.check(KV.lib.kvdec_read_probe_sweep(KV.ptr(bufs[i]), nb, KV.ptr(sink), blocks, threads,
+                                                       mode, lds, KV.stream_of(sink)), "read_probe_sweep")
+            big = nb > (1 << 30)
+            ms, _ = (graph_time(pcall, len(bufs), Kms, ms_warm, replays=2, min_graph=1) if big
+                     else graph_time(pcall, len(bufs), K, Wu))
+            return round(ms * 1e3, 3)
+
+        nb0, b0 = probe_sets(0)
+        floor = {"note": "per-step floors on this box, in the paths' graph timing: launch_us = an empty launch "
+                         "of 256 workgroups x 512 threads; launch_us_kivi_lean / _kivi_wide = the same grid "
+                         "with the lean (512 threads, 71184 B LDS) and wide (1024 threads, 150272 B LDS) KIVI "
+                         "kernels' block and LDS sizes; read_floor_us per path = the fastest plain streaming "
+                         "read of the path's algorithmic bytes found by kvdec_read_probe_sweep (the best probe "
+                         "form, not a proven bound: a kernel can beat it); frac_of_read_floor = read_floor_us / "
+                         "us_per_step",
+                 "launch_us": probe_us(nb0, b0, 256, 512, 0),
+                 "launch_us_kivi_lean": probe_us(nb0, b0, 256, 512, 0, 71184),
+                 "launch_us_kivi_wide": probe_us(nb0, b0, 256, 1024, 0, 150272)}
+        del b0
+        best_cfgs = [(512, 512, 0), (1024, 512, 0)]
+        head_bytes = (out.get("kivi_w256") or out.get("kivi_w256_chain") or {}).get("alg_bytes")
+        if head_bytes:
+            nb, bufs = probe_sets(head_bytes)
+            res = {}
+            for blocks in (256, 512, 1024, 2048):
+                for threads in (256, 512, 1024):
+                    for mode in range(8):
+                        res[(blocks, threads, mode)] = probe_us(nb, bufs, blocks, threads, mode)
+            del bufs
+            order = sorted(res, key=res.get)
+            floor["sweep_kivi_w256"] = {"bytes": nb, "best": cfg_name(*order[0]), "best_us": res[order[0]],
+                                        "us": {cfg_name(*c): res[c] for c in order}}
+            best_cfgs = list(dict.fromkeys(order[:4] + best_cfgs))
+            progress(f"floor sweep: best {cfg_name(*order[0])} {res[order[0]]} us")
+        probed = {}
         for name, rec in list(out.items()):
-            if rec.get("alg_bytes"):
-                rec["read_floor_us"] = probe_us(rec["alg_bytes"])
+            if rec.get("alg_bytes") in probed:
+                rec.update(probed[rec["alg_bytes"]])
                 rec["frac_of_read_floor"] = round(rec["read_floor_us"] / rec["us_per_step"], 4)
+            elif rec.get("alg_bytes"):
+                nb, bufs = probe_sets(rec["alg_bytes"])
+                tried = {c: probe_us(nb, bufs, *c) for c in best_cfgs
+                         if (c[2] & 3) < 2 or -(-nb // c[0]) < (1 << 31)}
+                del bufs
+                c = min(tried, key=tried.get)
+                rec["read_floor_us"] = tried[c]
+                rec["read_floor_config"] = cfg_name(*c)
+                rec["frac_of_read_floor"] = round(rec["read_floor_us"] / rec["us_per_step"], 4)
+                probed[rec["alg_bytes"]] = {"read_floor_us": tried[c], "read_floor_config": cfg_name(*c)}
         torch.cuda.empty_cache()
         progress("floors done")
 

@@ -374,6 +374,31 @@ int kvdec_dequant_v_tile(const void* packed, const void* scale,
  */
 int kvdec_read_probe(const void* src, int64_t bytes, void* sink, int32_t blocks, void* stream);
 
+/*
+ * The read probe's sweep form, no counterpart in the reference: `threads`
+ * (256, 512 or 1024) per workgroup, each workgroup one contiguous share;
+ * mode bits 0..1 pick the load (0 global non-temporal, 1 global, 2 buffer
+ * with the decode streams' non-temporal hint, 3 buffer without it), bit 2
+ * issues up to 16 loads per thread before any is used (else 4 in flight);
+ * `lds_bytes` (<= 160 KiB) of dynamic LDS are reserved and not touched, so
+ * that bytes = 0 times an empty launch with a decode kernel's grid, block
+ * and LDS footprint.  Buffer modes need each share below 2 GiB.
+ */
+int kvdec_read_probe_sweep(const void* src, int64_t bytes, void* sink, int32_t blocks,
+                           int32_t threads, int32_t mode, int32_t lds_bytes, void* stream);
+
+/*
+ * Kernel clock, no counterpart in the reference.  In the timing build
+ * (libkvdec_clock.so, the same sources compiled with -DKVDEC_CLOCK) every
+ * attention-kernel launch after this call takes the next of `slots` slots
+ * of `log` (cyclically): device memory of slots x 1024 x 2 uint64, zeroed
+ * by the caller.  Workgroup w < 1024 of the launch stores the GPU realtime
+ * counter (100 MHz) at its start into [slot][w][0] and after its output
+ * store into [slot][w][1].  log = NULL disarms.  The product library
+ * returns KVDEC_E_UNSUPPORTED.
+ */
+int kvdec_clock_arm(void* log, int32_t slots);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,6 +4,10 @@ The library is loaded from this directory; there is no fallback: importing a
 wrapper module when the library has not been built raises ImportError with the
 build command.  Negative return codes (host-side validation) become
 ValueError, positive ones (HIP launch errors) RuntimeError.
+
+KVDEC_LIBRARY=clock in the environment loads the timing build
+libkvdec_clock.so instead (the same kernels, which also record the GPU
+realtime counter at their start and end; see kvdec_clock_arm).
 """
 
 from __future__ import annotations
@@ -18,7 +22,11 @@ import os
 import torch  # noqa: F401
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkvdec.so")
+_LIBRARIES = {"": "libkvdec.so", "clock": "libkvdec_clock.so"}
+_which = os.environ.get("KVDEC_LIBRARY", "")
+if _which not in _LIBRARIES:
+    raise ImportError(f"KVDEC_LIBRARY={_which!r}: expected one of {sorted(_LIBRARIES)}")
+LIB_PATH = os.path.join(_HERE, _LIBRARIES[_which])
 
 # element types / layouts / workspace kinds (include/kvdec.h)
 F16, F32, BF16 = 0, 1, 2
@@ -42,6 +50,8 @@ SIGNATURES = {
     "kvdec_dense_decode_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32,
                                                   _i64, _i32, _f32, _vp]),
     "kvdec_read_probe": (ctypes.c_int, [_vp, _i64, _vp, _i32, _vp]),
+    "kvdec_read_probe_sweep": (ctypes.c_int, [_vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "kvdec_clock_arm": (ctypes.c_int, [_vp, _i32]),
     "kvdec_sparse_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32, _i64,
                                            _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
     "kvdec_paged_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _i64, _i32, _i32,

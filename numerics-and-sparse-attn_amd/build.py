@@ -6,6 +6,11 @@ Each HIP source is compiled for gfx950 only, with packed-fp32 instruction
 selection disabled; quant.hip additionally forbids FP contraction so its codes
 match the IEEE closed form bit for bit.  The shared library lands next to this
 file, where the ctypes loader (_kvdec.py) looks for it.
+
+The same sources also make libkvdec_clock.so, the timing build: attn.hip
+compiled with -DKVDEC_CLOCK, whose attention kernels record the GPU realtime
+counter at their start and end into a log armed by kvdec_clock_arm (the
+loader takes it when KVDEC_LIBRARY=clock; bench.py --kernel-clock).
 """
 
 from __future__ import annotations
@@ -25,6 +30,17 @@ ARCH = "gfx950"
 SOURCES = (
     ("attn.hip", []),
     ("quant.hip", ["-ffp-contract=off"]),
+)
+CLOCK_LIB_PATH = os.path.join(HERE, "libkvdec_clock.so")
+# object name, source, extra flags; each library links the objects it names
+OBJECTS = (
+    ("attn", "attn.hip", []),
+    ("attn_clock", "attn.hip", ["-DKVDEC_CLOCK"]),
+    ("quant", "quant.hip", ["-ffp-contract=off"]),
+)
+LIBRARIES = (
+    (LIB_PATH, ("attn", "quant")),
+    (CLOCK_LIB_PATH, ("attn_clock", "quant")),
 )
 
 COMMON_FLAGS = [
@@ -55,37 +71,39 @@ def _filter_host_feature_warning(text: str) -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link libkvdec.so; returns its path."""
+    """Compile every HIP source and link libkvdec.so and the timing build
+    libkvdec_clock.so; returns the product library's path."""
     hipcc = _hipcc()
     os.makedirs(BUILD_DIR, exist_ok=True)
     procs = []
-    objs = []
-    for src, extra in SOURCES:
-        obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+    objs = {}
+    for name, src, extra in OBJECTS:
+        obj = os.path.join(BUILD_DIR, name + ".o")
         cmd = [hipcc, *COMMON_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
-        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
-        objs.append(obj)
+        procs.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        objs[name] = obj
     failed = []
-    for src, p in procs:
+    for name, p in procs:
         out, _ = p.communicate()
         out = _filter_host_feature_warning(out)
         if out.strip() and (verbose or p.returncode):
             print(out, file=sys.stderr)
         if p.returncode:
-            failed.append(src)
+            failed.append(name)
     if failed:
         raise RuntimeError(f"hipcc failed on {', '.join(failed)}")
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    if r.returncode:
-        print(r.stdout, file=sys.stderr)
-        raise RuntimeError("linking libkvdec.so failed")
-    os.replace(tmp, LIB_PATH)
+    for lib, names in LIBRARIES:
+        tmp = lib + ".tmp"
+        cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[objs[n] for n in names]]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        if r.returncode:
+            print(r.stdout, file=sys.stderr)
+            raise RuntimeError(f"linking {os.path.basename(lib)} failed")
+        os.replace(tmp, lib)
     return LIB_PATH
 
 

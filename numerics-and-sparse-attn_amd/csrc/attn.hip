@@ -42,6 +42,33 @@ namespace {
 constexpr int kWaves = 8;                        // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 
+// Kernel clock, compiled only into the timing build (libkvdec_clock.so,
+// -DKVDEC_CLOCK; the product library has none of it).  Every launch of an
+// attention kernel gets slot `id` of a log armed by kvdec_clock_arm, with
+// one record per workgroup (the first kClockWgs): thread 0 stores the GPU's
+// constant-rate realtime counter when the workgroup starts and after its
+// output store, with plain vector stores (no atomics, no shared address).
+// The host reduces a slot to the launch's first start and last end, i.e.
+// its own duration with no profiler in the process, and the gap to the
+// next launch.
+#ifdef KVDEC_CLOCK
+constexpr int kClockWgs = 1024;
+struct ClockRef {
+  unsigned long long* log;
+  int id;
+};
+__device__ __forceinline__ void clock_stamp(const ClockRef& c, int end) {
+  if (c.log != nullptr && threadIdx.x == 0 && blockIdx.x < (unsigned)kClockWgs) {
+    const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+    c.log[((size_t)c.id * kClockWgs + blockIdx.x) * 2 + end] = t;
+  }
+}
+#define KVDEC_CLOCK_FIELD ClockRef clk;
+#define CLOCK_STAMP(args, end) clock_stamp((args).clk, end)
+#else
+#define KVDEC_CLOCK_FIELD
+#define CLOCK_STAMP(args, end) ((void)0)
+#endif
 
 struct AttnCommon {
   const _Float16* q;     // [B, H, 128]
@@ -52,6 +79,7 @@ struct AttnCommon {
   int32_t n_tiles, tiles_per_split, n_splits;
   float scale_log2;
   SlotRanges R;
+  KVDEC_CLOCK_FIELD
 };
 
 // LDS of a workgroup (bytes): two work counters, the per-wave max / sum of
@@ -136,7 +164,7 @@ struct QItems {
     Q.vp = s ? sinkq.vp : winq.vp;
     Q.vs = s ? sinkq.vs : winq.vs;
     Q.vz = s ? sinkq.vz : winq.vz;
-    load_q_raw(Q, s ? 0 : i, i < n, lane, X);
+    load_q_raw(Q, s ? 0 : i, i < n, lane, X, s ? sink : kTile);
   }
   __device__ __forceinline__ void step(int i, const Raw& X, State& s, const StepCtx& c) const {
     const bool sk = i == n - 1;
@@ -318,6 +346,7 @@ __device__ __forceinline__ void merge_out(const AttnCommon& P, char* lds, int64_
       P.ws[total * kHeadDim + total + idx] = L;
     }
   }
+  CLOCK_STAMP(P, 1);
 }
 
 // Validity ranges of the [sink + window] cache at this length (the
@@ -817,17 +846,19 @@ struct packs_q<Src, decltype((void)Src::kPackQ)> {
 template <class Src>
 __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) {
   extern __shared__ __align__(16) char lds[];
+  CLOCK_STAMP(P, 0);
   // Bring every 64-byte line of the kernel arguments into the scalar cache
   // in one round trip: the compiler fetches the fields where they are first
   // used, which would otherwise cost a cache miss per line in series.
   {
     constexpr int kArgLines = (int)(sizeof(AttnCommon) + sizeof(Src) + 63) / 64;
-    static_assert(kArgLines <= 6, "kernel arguments span more lines than are touched");
+    static_assert(kArgLines <= 8, "kernel arguments span more lines than are touched");
     const cint32* ka = (const cint32*)__builtin_amdgcn_kernarg_segment_ptr();
-    int32_t x[6];
+    int32_t x[8];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
+    for (int i = 0; i < 8; ++i) x[i] = i < kArgLines ? ka[16 * i] : 0;
     asm volatile("" ::"s"(x[0]), "s"(x[1]), "s"(x[2]), "s"(x[3]), "s"(x[4]), "s"(x[5]));
+    if constexpr (kArgLines > 6) asm volatile("" ::"s"(x[6]), "s"(x[7]));
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -895,6 +926,7 @@ struct LeanCommon {
   float scale_log2;
   int G;
   SlotRanges R;
+  KVDEC_CLOCK_FIELD
 };
 
 // The first part of every lean kernel: kernel-argument lines fetched in one
@@ -951,9 +983,10 @@ __device__ __forceinline__ void q_quarter_store(char* qarea, int quarter, int la
 // The Q area's readiness count (quarters stored), in the word after it:
 // zeroed before a workgroup barrier that precedes every increment,
 // incremented (release, one lane) by each wave that stored its quarter,
-// polled (acquire) before the operand is read.  The poll is bounded (~10^7
-// cycles; the four storing waves run unconditionally, so it ends long
-// before that).
+// polled (acquire) before the operand is read.  The poll is bounded: 2^16
+// reads with an s_sleep 1 (~64 cycles) after each, ~4 x 10^6 cycles or
+// ~2 ms (the four storing waves run unconditionally and their quarters
+// arrive within microseconds, so it ends long before that).
 __device__ __forceinline__ void q_quarter_ready(char* qarea, int lane) {
   if (lane == 0)
     __hip_atomic_fetch_add(reinterpret_cast<int*>(qarea + kQAreaBytes), 1, __ATOMIC_RELEASE,
@@ -1022,6 +1055,7 @@ __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds,
   half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
               (_Float16)(acc[3] * inv)};
   store_out4(C.o + ((size_t)head * C.G + hn) * kHeadDim + 4 * ch, h);
+  CLOCK_STAMP(C, 1);
 }
 
 __device__ __forceinline__ void lean_publish_ml(int G, WaveState& st, char* lds, int lane, int wave) {
@@ -1050,6 +1084,7 @@ struct F16LeanArgs {
 
 __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
   extern __shared__ __align__(16) char lds[];
+  CLOCK_STAMP(A.c, 0);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t head = blockIdx.x;
@@ -1135,7 +1170,7 @@ struct KiviLeanArgs {
   QRegion winq;          // [heads][nwt] groups
   uint32_t res_bytes;    // whole-tensor sizes, each < 2^31
   int res_rows;          // residual rows per KV head (<= 128)
-  uint32_t win_code_bytes, win_meta_bytes, sink_code_bytes, sink_meta_bytes;
+  uint32_t win_code_bytes, win_meta_bytes;
   int nwt;               // window-old groups (<= 7)
   int sink;
 };
@@ -1143,6 +1178,7 @@ struct KiviLeanArgs {
 template <bool PACK>
 __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) {
   extern __shared__ __align__(16) char lds[];
+  CLOCK_STAMP(A.c, 0);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t head = blockIdx.x;
@@ -1163,9 +1199,9 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     // item i < nwt: window-old group i; item nwt: the sink group
     auto load = [&](int i, QTileRaw& X) {
       const bool sk = i == nwt;
-      const QTensors T = sk ? q_tensors(A.sinkq, A.sink_code_bytes, A.sink_meta_bytes)
+      const QTensors T = sk ? q_sink_tensors(A.sinkq, head, A.sink)
                             : q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
-      load_q_group(T, sk ? head : head * (uint32_t)nwt + (uint32_t)i, i < n_q, lane, X);
+      load_q_group(T, sk ? 0u : head * (uint32_t)nwt + (uint32_t)i, i < n_q, lane, X);
     };
     // A wave whose second item is the sink group loads and steps it first:
     // its few bytes arrive early, and the wave's last step is no longer the
@@ -1255,6 +1291,7 @@ __device__ __forceinline__ void wide_publish_ml(int G, WaveState& st, char* lds,
 template <bool PACK>
 __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs A) {
   extern __shared__ __align__(16) char lds[];
+  CLOCK_STAMP(A.c, 0);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t head = blockIdx.x;
@@ -1264,11 +1301,11 @@ __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs
   int* ctr = reinterpret_cast<int*>(lds + kWideLdsCtr);
   const int nwt = A.nwt, n_q = nwt + 1;
   const QTensors Tw = q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
-  const QTensors Ts = q_tensors(A.sinkq, A.sink_code_bytes, A.sink_meta_bytes);
+  const QTensors Ts = q_sink_tensors(A.sinkq, head, A.sink);
   // item i < nwt: window-old group i; item nwt: the sink group
   auto load = [&](int i, QTileRaw& X) {
     const bool sk = i == nwt;
-    load_q_group(sk ? Ts : Tw, sk ? head : head * (uint32_t)nwt + (uint32_t)i, i < n_q, lane, X);
+    load_q_group(sk ? Ts : Tw, sk ? 0u : head * (uint32_t)nwt + (uint32_t)i, i < n_q, lane, X);
   };
   if (threadIdx.x == 0) *ctr = kWideQWaves;
   QTileRaw X;
@@ -1363,6 +1400,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs
   half4v h = {(_Float16)(acc[0] * inv), (_Float16)(acc[1] * inv), (_Float16)(acc[2] * inv),
               (_Float16)(acc[3] * inv)};
   store_out4(A.c.o + ((size_t)head * A.c.G + hn) * kHeadDim + 4 * ch, h);
+  CLOCK_STAMP(A.c, 1);
 }
 
 // Streaming read of `n16` 16-byte words, for the measurement of a decode
@@ -1390,6 +1428,73 @@ __global__ __launch_bounds__(kThreads) void read_probe_kernel(const u32x4* src, 
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) r ^= red[w];
     sink[blockIdx.x] = r;
+  }
+}
+
+// The read probe's sweep form: THREADS threads per workgroup, each
+// workgroup one contiguous share; KIND 0 global non-temporal loads, 1 plain
+// global loads, 2 buffer loads with the decode streams' non-temporal hint,
+// 3 buffer loads without it; UPFRONT: each thread issues up to 16 loads
+// before it uses any (else 4 in flight per loop turn).  The dynamic LDS the
+// launch reserves is not touched: it only gives the launch a decode
+// kernel's LDS footprint.
+template <int KIND>
+__device__ __forceinline__ u32x4 probe_load(const u32x4* src, rsrc_t r, int64_t i, int64_t b, int64_t e) {
+  if constexpr (KIND == 0) return i < e ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+  if constexpr (KIND == 1) return i < e ? src[i] : u32x4{0u, 0u, 0u, 0u};
+  const uint32_t off = i < e ? (uint32_t)(i - b) * 16u : kOOB;
+  if constexpr (KIND == 2) return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+template <int THREADS, int KIND, bool UPFRONT>
+__global__ __launch_bounds__(THREADS) void read_probe2_kernel(const u32x4* src, int64_t n16, uint32_t* sink) {
+  const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+  const int64_t b = (int64_t)blockIdx.x * per;
+  const int64_t e = b + per < n16 ? b + per : n16;
+  const rsrc_t r = make_rsrc(src + (b < n16 ? b : 0), e > b ? (uint32_t)((e - b) * 16) : 0u);
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  constexpr int kIn = UPFRONT ? 16 : 4;
+  for (int64_t i = b + threadIdx.x; i < e; i += kIn * THREADS) {
+    u32x4 x[kIn];
+#pragma unroll
+    for (int u = 0; u < kIn; ++u) x[u] = probe_load<KIND>(src, r, i + u * THREADS, b, e);
+#pragma unroll
+    for (int u = 0; u < kIn; ++u) acc ^= x[u];
+  }
+  uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  __shared__ uint32_t red[THREADS / 64];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v ^= (uint32_t)__shfl_xor((int)v, off);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t q = 0;
+#pragma unroll
+    for (int w = 0; w < THREADS / 64; ++w) q ^= red[w];
+    sink[blockIdx.x] = q;
+  }
+}
+
+template <int THREADS, int KIND>
+void launch_probe2(bool upfront, unsigned blocks, size_t lds, hipStream_t st, const u32x4* src, int64_t n16,
+                   uint32_t* sink) {
+  if (upfront)
+    hipLaunchKernelGGL((read_probe2_kernel<THREADS, KIND, true>), dim3(blocks), dim3(THREADS), lds, st, src, n16,
+                       sink);
+  else
+    hipLaunchKernelGGL((read_probe2_kernel<THREADS, KIND, false>), dim3(blocks), dim3(THREADS), lds, st, src, n16,
+                       sink);
+}
+
+template <int THREADS>
+void launch_probe2_kind(int kind, bool upfront, unsigned blocks, size_t lds, hipStream_t st, const u32x4* src,
+                        int64_t n16, uint32_t* sink) {
+  switch (kind) {
+    case 0: launch_probe2<THREADS, 0>(upfront, blocks, lds, st, src, n16, sink); break;
+    case 1: launch_probe2<THREADS, 1>(upfront, blocks, lds, st, src, n16, sink); break;
+    case 2: launch_probe2<THREADS, 2>(upfront, blocks, lds, st, src, n16, sink); break;
+    default: launch_probe2<THREADS, 3>(upfront, blocks, lds, st, src, n16, sink); break;
   }
 }
 
@@ -1471,6 +1576,26 @@ int launch_status() {
   return e == hipSuccess ? KVDEC_OK : (int)e;
 }
 
+// The timing build's launch counter: each attention launch takes the next
+// slot of the armed log (slots are reused cyclically), none while disarmed.
+#ifdef KVDEC_CLOCK
+std::mutex g_clock_mu;
+unsigned long long* g_clock_log = nullptr;
+int g_clock_slots = 0, g_clock_next = 0;
+ClockRef next_clock() {
+  std::lock_guard<std::mutex> lock(g_clock_mu);
+  ClockRef c{g_clock_log, 0};
+  if (g_clock_log != nullptr) {
+    c.id = g_clock_next;
+    g_clock_next = g_clock_next + 1 == g_clock_slots ? 0 : g_clock_next + 1;
+  }
+  return c;
+}
+#define SET_CLOCK(args) ((args).clk = next_clock())
+#else
+#define SET_CLOCK(args) ((void)0)
+#endif
+
 template <class Src>
 int launch_attn(AttnCommon P, const Src& S, bool kivi, size_t ws_bytes, hipStream_t stream) {
   // The KIVI plan never splits: its quantized and residual regions are
@@ -1484,6 +1609,7 @@ int launch_attn(AttnCommon P, const Src& S, bool kivi, size_t ws_bytes, hipStrea
   }
   const int64_t blocks = P.pairs * plan.splits;
   if (blocks > 0x7fffffffLL) return KVDEC_E_SHAPE;
+  SET_CLOCK(P);
   hipLaunchKernelGGL((attn_kernel<Src>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, stream,
                      P, S);
   int rc = launch_status();
@@ -1518,6 +1644,7 @@ int launch_f16_lean(const AttnCommon& P, const _Float16* k, const _Float16* v, i
   A.k = k;
   A.v = v;
   A.rows = rows;
+  SET_CLOCK(A.c);
   hipLaunchKernelGGL(f16_lean_kernel, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes + kQLdsBytes, stream, A);
   return launch_status();
 }
@@ -1635,10 +1762,9 @@ int kivi_decode_t(const void* q, const void* k_res, const void* v_res, const voi
     A.res_rows = res_rows;
     A.win_code_bytes = (uint32_t)(P.pairs * S.nwt * 1024);
     A.win_meta_bytes = (uint32_t)(P.pairs * S.nwt * 256);
-    A.sink_code_bytes = (uint32_t)(P.pairs * 1024);
-    A.sink_meta_bytes = (uint32_t)(P.pairs * 256);
     A.nwt = S.nwt;
     A.sink = sink;
+    SET_CLOCK(A.c);
     if (lean)
       hipLaunchKernelGGL(kivi_lean_kernel<PACK>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes + kQLdsBytes, st, A);
     else if constexpr (PACK)
@@ -1876,6 +2002,21 @@ const char* kvdec_strerror(int code) {
 
 const char* kvdec_version(void) { return "kvdec 0.3 gfx950"; }
 
+int kvdec_clock_arm(void* log, int32_t slots) {
+#ifdef KVDEC_CLOCK
+  if (log != nullptr && slots < 1) return KVDEC_E_SHAPE;
+  std::lock_guard<std::mutex> lock(g_clock_mu);
+  g_clock_log = static_cast<unsigned long long*>(log);
+  g_clock_slots = log != nullptr ? slots : 0;
+  g_clock_next = 0;
+  return KVDEC_OK;
+#else
+  (void)log;
+  (void)slots;
+  return KVDEC_E_UNSUPPORTED;   // the product library has no kernel clock
+#endif
+}
+
 int kvdec_num_splits(int kind, int64_t B, int32_t KVH, int64_t n_slots) {
   if (B < 1 || KVH < 1 || n_slots < 1) return 1;
   if (kind == KVDEC_KIND_KIVI) return 1;
@@ -1918,6 +2059,29 @@ int kvdec_read_probe(const void* src, int64_t bytes, void* sink, int32_t blocks,
   if (bytes < 0 || bytes % 16 != 0 || blocks < 1 || blocks > 65536) return KVDEC_E_SHAPE;
   hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
                      static_cast<const u32x4*>(src), bytes / 16, static_cast<uint32_t*>(sink));
+  return launch_status();
+}
+
+int kvdec_read_probe_sweep(const void* src, int64_t bytes, void* sink, int32_t blocks, int32_t threads,
+                           int32_t mode, int32_t lds_bytes, void* stream) {
+  if (!sink || (bytes > 0 && !src)) return KVDEC_E_NULL;
+  if (bytes < 0 || bytes % 16 != 0 || blocks < 1 || blocks > 65536) return KVDEC_E_SHAPE;
+  if (threads != 256 && threads != 512 && threads != 1024) return KVDEC_E_SHAPE;
+  if (mode < 0 || mode > 7 || lds_bytes < 0 || lds_bytes > 160 * 1024) return KVDEC_E_SHAPE;
+  const int kind = mode & 3;
+  const bool upfront = (mode & 4) != 0;
+  const int64_t n16 = bytes / 16, per = (n16 + blocks - 1) / blocks;
+  if (kind >= 2 && per * 16 >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;   // 31-bit buffer offsets
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const u32x4* s = static_cast<const u32x4*>(src);
+  uint32_t* k = static_cast<uint32_t*>(sink);
+  const size_t lds = (size_t)lds_bytes;
+  if (threads == 256)
+    launch_probe2_kind<256>(kind, upfront, (unsigned)blocks, lds, st, s, n16, k);
+  else if (threads == 512)
+    launch_probe2_kind<512>(kind, upfront, (unsigned)blocks, lds, st, s, n16, k);
+  else
+    launch_probe2_kind<1024>(kind, upfront, (unsigned)blocks, lds, st, s, n16, k);
   return launch_status();
 }
 

@@ -510,17 +510,40 @@ __device__ __forceinline__ void load_q_group(const QTensors& T, uint32_t n, bool
   X.vz = bload4(T.vz, l4, om);
 }
 
-// Issue the loads of tile tq of region Q (valid == false: zeros, no access).
+// Bytes of a group's pieces that hold its first `rows` tokens: K code byte
+// rows of 4 tokens x 128 channels, V code rows of 32 bytes, V scale / zero
+// rows of 4 fp16 (the K scales and zeros are per channel: all 256 bytes).
+// A sink group holds `sink` real tokens padded to 32 with copies of token 0
+// (quant_kernel.py:602-606); its padding is masked in the decode, so only
+// these rows are read and the rest return zeros without a memory access.
+__device__ __forceinline__ uint32_t q_kcode_bytes(int rows) { return 128u * (uint32_t)((rows + 3) / 4); }
+__device__ __forceinline__ uint32_t q_vcode_bytes(int rows) { return 32u * (uint32_t)rows; }
+__device__ __forceinline__ uint32_t q_vmeta_bytes(int rows) { return 8u * (uint32_t)rows; }
+
+// Resources over the sink group of KV head `head` alone (group `head` of
+// the sink tensors), sized to its `sink` real tokens; load it as group 0.
+__device__ __forceinline__ QTensors q_sink_tensors(const QRegion& Q, uint32_t head, int sink) {
+  return QTensors{make_rsrc(Q.kp + (size_t)head * 1024, q_kcode_bytes(sink)),
+                  make_rsrc(Q.vp + (size_t)head * 1024, q_vcode_bytes(sink)),
+                  make_rsrc(Q.ks + (size_t)head * kHeadDim, 256u),
+                  make_rsrc(Q.kz + (size_t)head * kHeadDim, 256u),
+                  make_rsrc(Q.vs + (size_t)head * 128, q_vmeta_bytes(sink)),
+                  make_rsrc(Q.vz + (size_t)head * 128, q_vmeta_bytes(sink))};
+}
+
+// Issue the loads of tile tq of region Q (valid == false: zeros, no access),
+// reading only the rows of its first `rows` tokens (32: the whole group).
 __device__ __forceinline__ void load_q_raw(const QRegion& Q, int tq, bool valid, int lane,
-                                           QTileRaw& X) {
+                                           QTileRaw& X, int rows = kTile) {
   const size_t t = valid ? (size_t)tq : 0;
-  const uint32_t n16 = valid ? 1024u : 0u, n4 = valid ? 256u : 0u;
-  X.kc = bload16(make_rsrc(Q.kp + t * 1024, n16), 16u * lane);
-  X.vc = bload16(make_rsrc(Q.vp + t * 1024, n16), 16u * lane);
-  X.ks = bload4(make_rsrc(Q.ks + t * kHeadDim, n4), 4u * lane);
-  X.kz = bload4(make_rsrc(Q.kz + t * kHeadDim, n4), 4u * lane);
-  X.vs = bload4(make_rsrc(Q.vs + t * 128, n4), 4u * lane);
-  X.vz = bload4(make_rsrc(Q.vz + t * 128, n4), 4u * lane);
+  const uint32_t nk = valid ? q_kcode_bytes(rows) : 0u, nv = valid ? q_vcode_bytes(rows) : 0u;
+  const uint32_t nks = valid ? 256u : 0u, nvs = valid ? q_vmeta_bytes(rows) : 0u;
+  X.kc = bload16(make_rsrc(Q.kp + t * 1024, nk), 16u * lane);
+  X.vc = bload16(make_rsrc(Q.vp + t * 1024, nv), 16u * lane);
+  X.ks = bload4(make_rsrc(Q.ks + t * kHeadDim, nks), 4u * lane);
+  X.kz = bload4(make_rsrc(Q.kz + t * kHeadDim, nks), 4u * lane);
+  X.vs = bload4(make_rsrc(Q.vs + t * 128, nvs), 4u * lane);
+  X.vz = bload4(make_rsrc(Q.vz + t * 128, nvs), 4u * lane);
 }
 
 // Accumulators of the KIVI tiles, kept beside WaveState (whose m and l they

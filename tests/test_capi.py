@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 22
+    assert len(funcs) == 24
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -134,6 +134,35 @@ def test_read_probe_validation():
     assert probe(FAKE, -16, FAKE, 256, None) == E["SHAPE"]
     assert probe(FAKE, 1024, FAKE, 0, None) == E["SHAPE"]
     assert probe(FAKE, 1024, FAKE, 65537, None) == E["SHAPE"]
+
+
+def test_read_probe_sweep_validation():
+    """The sweep form of the probe rejects bad sizes, block sizes, modes and
+    LDS reservations before launching anything."""
+    probe = K.lib.kvdec_read_probe_sweep
+    assert probe(FAKE, 1024, None, 256, 512, 0, 0, None) == E["NULL"]
+    assert probe(None, 1024, FAKE, 256, 512, 0, 0, None) == E["NULL"]
+    assert probe(FAKE, 1000, FAKE, 256, 512, 0, 0, None) == E["SHAPE"]
+    assert probe(FAKE, 1024, FAKE, 0, 512, 0, 0, None) == E["SHAPE"]
+    for threads in (0, 64, 128, 768, 2048):
+        assert probe(FAKE, 1024, FAKE, 256, threads, 0, 0, None) == E["SHAPE"]
+    for mode in (-1, 8):
+        assert probe(FAKE, 1024, FAKE, 256, 512, mode, 0, None) == E["SHAPE"]
+    assert probe(FAKE, 1024, FAKE, 256, 512, 0, -1, None) == E["SHAPE"]
+    assert probe(FAKE, 1024, FAKE, 256, 512, 0, 160 * 1024 + 1, None) == E["SHAPE"]
+    # buffer loads address a workgroup's share with 31-bit offsets
+    assert probe(FAKE, 1 << 32, FAKE, 1, 512, 2, 0, None) == E["SHAPE"]
+
+
+def test_clock_arm_only_in_timing_build():
+    """The kernel clock exists only in the timing build; the product
+    library says so instead of recording anything."""
+    if os.path.basename(K.LIB_PATH) == "libkvdec.so":
+        assert K.lib.kvdec_clock_arm(FAKE, 16) == E["UNSUPPORTED"]
+        assert K.lib.kvdec_clock_arm(None, 0) == E["UNSUPPORTED"]
+    else:
+        assert K.lib.kvdec_clock_arm(FAKE, 0) == E["SHAPE"]
+        assert K.lib.kvdec_clock_arm(None, 0) == 0
 
 
 def _sparse(**kw):

@@ -363,3 +363,54 @@ def test_quantized_attention_sink_sizes(sink, W, device):
         assert max_abs(o, ref) < ATTN_TOL
         if L > sink + W:
             assert_nearly_rounded(o, ref)
+
+
+@pytest.mark.parametrize("W", [256, 1024])
+def test_kivi_bit_identical_under_concurrent_load(W, device):
+    """The fused decode's waves meet only at the Q readiness count (lean
+    kernel), the group-queue counter (16-wave kernel) and the merge barrier,
+    so a result must not depend on how far each wave has got.  Launches made
+    while a second stream (default priority) copies 512 MiB through the same
+    CUs and HBM must be bit-identical to a launch on an idle GPU (the lean
+    kernel's work split is static; the 16-wave kernel's queue makes the
+    summation order vary, so there the outputs must agree within the
+    attention gate and the oracle's)."""
+    from quant_kernel import build_quantized_kv_cache, sparse_decode_attention_quantized
+    B, H, KVH, D = 32, 64, 8, 128
+    L = S + W + 1000
+    gen = torch.Generator(device=device).manual_seed(70 + W)
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    cache = build_quantized_kv_cache(kc, vc)
+    args = [cache[k] for k in O.CACHE_KEYS]
+
+    def attend():
+        return sparse_decode_attention_quantized(q, *args, seq_len=L, window=W)
+
+    say(f"kivi concurrent-load determinism W={W}")
+    ref = attend()
+    torch.cuda.synchronize()
+    src = torch.ones((512 << 20) // 4, dtype=torch.int32, device=device)
+    dst = torch.empty_like(src)
+    side = torch.cuda.Stream(device)
+    outs = []
+    for i in range(24):
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            dst.copy_(src)
+        if i % 3:
+            outs.append(attend())
+        else:
+            torch.cuda.current_stream(device).wait_stream(side)
+            outs.append(attend())
+    torch.cuda.synchronize()
+    o_ref = host(ref)
+    for i, o in enumerate(outs):
+        if W <= 352:
+            assert torch.equal(o, ref), f"launch {i} differs from the idle-GPU launch"
+        else:
+            assert max_abs(host(o), o_ref) < 1e-3, f"launch {i}"
+    hc = _host_cache(cache)
+    ho = O.quantized_attention(host(q)[:2], W - R, {k: v[:2] for k, v in hc.items()}, SCALE)
+    assert max_abs(o_ref[:2], ho) < ATTN_TOL

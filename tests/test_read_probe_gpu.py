@@ -34,3 +34,22 @@ def test_read_probe_xor(n16, blocks):
     K.check(K.lib.kvdec_read_probe(K.ptr(src), 16 * n16, K.ptr(sink), blocks, K.stream_of(sink)), "read_probe")
     got = sink.cpu().numpy().view(np.uint32)
     np.testing.assert_array_equal(got, _expected(words, blocks))
+
+
+@pytest.mark.parametrize("threads", [256, 512, 1024])
+@pytest.mark.parametrize("mode", range(8))
+@pytest.mark.parametrize("n16,blocks", [(0, 256), (4095, 7), (65536 + 13, 256), (262144, 2048)])
+def test_read_probe_sweep_xor(n16, blocks, threads, mode):
+    """Every block size and load form of the sweep probe reads exactly its
+    share (buffer forms: past the share, zeros without an access)."""
+    say(f"read probe sweep n16={n16} blocks={blocks} threads={threads} mode={mode}")
+    rng = np.random.default_rng(n16 + blocks + threads + mode)
+    words = rng.integers(0, 2**32, size=4 * max(n16, 1), dtype=np.uint32)[: 4 * n16]
+    gpu = torch.device("cuda:0")
+    src = (torch.from_numpy(words.view(np.int32).copy()).to(gpu) if n16
+           else torch.empty(4, dtype=torch.int32, device=gpu))
+    sink = torch.full((blocks,), -1, dtype=torch.int32, device=gpu)
+    K.check(K.lib.kvdec_read_probe_sweep(K.ptr(src), 16 * n16, K.ptr(sink), blocks, threads, mode, 4096,
+                                         K.stream_of(sink)), "read_probe_sweep")
+    got = sink.cpu().numpy().view(np.uint32)
+    np.testing.assert_array_equal(got, _expected(words, blocks))

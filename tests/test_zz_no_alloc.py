@@ -24,6 +24,45 @@ def _inputs(B, H, KVH, L, seed, device):
     return q, k, v
 
 
+def test_noalloc_first_call_under_graph_capture(device):
+    """The entry point's first call in the process is made inside a HIP graph
+    capture (no other test calls it, and this one runs first in this file):
+    that call looks up the device array's address, and must neither fail
+    the capture nor allocate.  The graph is replayed three times, with eager
+    work between the replays and the output reset to NaN before each, and
+    every replay is bit-identical to the workspace entry point."""
+    import _kvdec as K
+    torch.cuda.set_device(device)
+    B, H, KVH, L = 2, 32, 2, 16384
+    q, k, v = _inputs(B, H, KVH, L, 3, device)
+    ws, nbytes = K.workspace(K.KIND_DENSE, B, H, KVH, L, 128, device)
+    o_ws = torch.empty_like(q)
+
+    def eager():
+        rc = K.lib.kvdec_dense_decode(K.ptr(q), K.ptr(k), K.ptr(v), K.ptr(o_ws), K.F16, B, H, KVH, L, 128,
+                                      SCALE, K.ptr(ws), nbytes, torch.cuda.current_stream(device).cuda_stream)
+        assert rc == 0, K.strerror(rc)
+
+    eager()
+    torch.cuda.synchronize()
+    o_na = torch.full_like(q, float("nan"))
+    say(f"noalloc under capture B={B} H={H} KVH={KVH} L={L}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = K.lib.kvdec_dense_decode_noalloc(K.ptr(q), K.ptr(k), K.ptr(v), K.ptr(o_na), K.F16, B, H, KVH, L,
+                                              128, SCALE, torch.cuda.current_stream(device).cuda_stream)
+    assert rc == 0, K.strerror(rc)
+    for r in range(3):
+        o_na.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o_na, o_ws), f"replay {r}"
+        eager()
+        torch.cuda.synchronize()
+    del g
+
+
 def test_noalloc_equals_workspace_entry_point(device):
     import _kvdec as K
     torch.cuda.set_device(device)
