@@ -369,6 +369,26 @@ def measured_traffic(key):
     return int(rec["fetch_bytes_per_launch"] + rec["write_bytes_per_launch"]), {**src, "status": "current"}
 
 
+def recorded_kernel_clock(key):
+    """The path's kernel-only duration recorded by the timing build
+    (bench.py --kernel-clock, profiles/kernel_clock.json): the mean over a
+    graph's launches of last workgroup end - first workgroup start, and the
+    mean gap to the next launch; None when nothing is recorded or the record
+    was measured on other kernel sources."""
+    src = {"file": "profiles/kernel_clock.json", "key": key, "current_source_sha16": kernel_source_hash()}
+    try:
+        with open(os.path.join(ROOT, "profiles", "kernel_clock.json")) as f:
+            rec = json.load(f).get("paths", {}).get(key)
+    except (OSError, ValueError):
+        rec = None
+    if rec is None:
+        return None, {**src, "status": "not recorded"}
+    src.update(recorded_source_sha16=rec.get("source_sha16"))
+    if rec.get("source_sha16") != src["current_source_sha16"]:
+        return None, {**src, "status": "stale: recorded on other kernel sources"}
+    return rec, {**src, "status": "current"}
+
+
 def n_sets(bytes_per_set):
     return int(max(1, min(MAX_SETS, -(-COLD_SET_BYTES // bytes_per_set))))
 
@@ -878,6 +898,15 @@ def main():
         "cpu_baseline": head_cpu,
         "paths": out,
     }
+    clk, clk_src = recorded_kernel_clock(head_key)
+    line["roofline"]["kernel_only"] = (
+        {"note": "achieved and frac over the kernel's own duration (first workgroup start to last "
+                 "workgroup end, timing build, no profiler), without the gap between launches that "
+                 "value includes", "kernel_us": clk["kernel_us_mean"],
+         "launch_gap_us": clk["gap_us_mean"],
+         "achieved": round(head["alg_bytes"] / (clk["kernel_us_mean"] * 1e-6) / 1e9, 1),
+         "frac": round(head["alg_bytes"] / (clk["kernel_us_mean"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+         "source": clk_src} if clk else {"source": clk_src})
     if floor is not None:
         line["floor"] = floor
     if grid is not None:
