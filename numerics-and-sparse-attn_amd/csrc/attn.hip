@@ -1018,35 +1018,57 @@ __device__ __forceinline__ void q_operand_read(const char* qarea, int lane, half
 // published partials into the fp16 output rows of this KV head.  Waves
 // below NPACK published packed quantized rows unfolded: their row hn + 8
 // (the remainder part) is added to row hn.
-template <int NPACK = 0>
+// LDS of a lean kernel with NW waves: the maxima and sums of every wave's
+// partial (16 heads each), then one 8 KB slot per wave; the Q area follows.
+// NW = 8 is attn_kernel's layout (kLdsM, kLdsL, kLdsSlots, kLdsBytes).
+template <int NW>
+struct LeanLds {
+  static constexpr int kM = kLdsM;
+  static constexpr int kL = kM + NW * kMaxGroup * 4;
+  static constexpr int kSlots = (kL + NW * kMaxGroup * 4 + 255) & ~255;
+  static constexpr int kBytes = kSlots + NW * kSlotBytes;
+};
+static_assert(LeanLds<kWaves>::kL == kLdsL && LeanLds<kWaves>::kSlots == kLdsSlots &&
+                  LeanLds<kWaves>::kBytes == kLdsBytes,
+              "the 8-wave lean layout is attn_kernel's");
+
+// Barrier, then one thread per (head, 4 channels) combines the NW waves'
+// published partials into the fp16 output rows of this KV head.  Waves
+// below NPACK, and the last wave when LASTPACK, published packed quantized
+// rows unfolded: their row hn + 8 (the remainder part) is added to row hn.
+template <int NPACK = 0, int NW = kWaves, bool LASTPACK = false>
 __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds, uint32_t head) {
+  typedef LeanLds<NW> Lds;
   __syncthreads();
-  const float* sh_m = reinterpret_cast<const float*>(lds + kLdsM);
-  const float* sh_l = reinterpret_cast<const float*>(lds + kLdsL);
+  const float* sh_m = reinterpret_cast<const float*>(lds + Lds::kM);
+  const float* sh_l = reinterpret_cast<const float*>(lds + Lds::kL);
   const int e = threadIdx.x;
   if (e >= C.G * 32) return;
   const int hn = e >> 5, ch = e & 31;
-  float mw[kWaves], lw[kWaves];
-  float4v ow[kWaves];
+  float mw[NW], lw[NW];
+  float4v ow[NW];
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < NW; ++w) {
     mw[w] = sh_m[w * kMaxGroup + hn];
     lw[w] = sh_l[w * kMaxGroup + hn];
-    ow[w] = *reinterpret_cast<const float4v*>(lds + kLdsSlots + w * kSlotBytes + row_off(hn, ch));
+    ow[w] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn, ch));
   }
-  float4v orem[NPACK > 0 ? NPACK : 1];
+  constexpr int kRem = NPACK + (LASTPACK ? 1 : 0);
+  float4v orem[kRem > 0 ? kRem : 1];
 #pragma unroll
-  for (int w = 0; w < NPACK; ++w)
-    orem[w] = *reinterpret_cast<const float4v*>(lds + kLdsSlots + w * kSlotBytes + row_off(hn + 8, ch));
+  for (int i = 0; i < kRem; ++i) {
+    const int w = i < NPACK ? i : NW - 1;
+    orem[i] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn + 8, ch));
+  }
 #pragma unroll
-  for (int w = 0; w < NPACK; ++w) ow[w] += orem[w];
+  for (int i = 0; i < kRem; ++i) ow[i < NPACK ? i : NW - 1] += orem[i];
   float M = mw[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, mw[w]);
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, mw[w]);
   float L = 0.f;
   float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const float f = __builtin_amdgcn_exp2f(mw[w] - M);
     L += lw[w] * f;
     acc += ow[w] * f;
@@ -1058,12 +1080,13 @@ __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds,
   CLOCK_STAMP(C, 1);
 }
 
+template <int NW = kWaves>
 __device__ __forceinline__ void lean_publish_ml(int G, WaveState& st, char* lds, int lane, int wave) {
   st.l = group_sum(st.l);
   const int n = lane & 15, g = lane >> 4;
   if (n < G && g == 0) {
-    reinterpret_cast<float*>(lds + kLdsM)[wave * kMaxGroup + n] = st.m;
-    reinterpret_cast<float*>(lds + kLdsL)[wave * kMaxGroup + n] = st.l;
+    reinterpret_cast<float*>(lds + LeanLds<NW>::kM)[wave * kMaxGroup + n] = st.m;
+    reinterpret_cast<float*>(lds + LeanLds<NW>::kL)[wave * kMaxGroup + n] = st.l;
   }
 }
 
@@ -1247,6 +1270,77 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     lean_publish_f(A.c.G, st, slot, lane);
   }
   lean_merge<PACK ? 4 : 0>(A.c, lds, head);   // PACK: waves 0..3 left their rows unfolded
+}
+
+// The lean KIVI kernel for exactly 4 window-old groups (W = 256 with
+// R = 128) with a ninth wave: waves 0..3 step window-old group w, wave 8 the
+// sink group, waves 4..7 residual tiles 0..3.  In the 8-wave kernel the
+// fifth quantized item (the sink group) falls to wave 0, whose two steps in
+// series (each ~1.3 us for a single wave on its SIMD) end the kernel last;
+// here the sink step runs in its own wave beside them (wave 8 shares SIMD 0
+// with waves 0 and 4; 136 VGPRs fit three waves per SIMD).  Measured per
+// step (interleaved A/B, two boxes): 5.78 -> 5.67 us and 5.79 -> 5.69 us.
+// With fewer window-old groups every quantized item already has a wave of
+// its own and the extra wave only costs (W = 160: 5.22 -> 5.43 us).
+constexpr int kLean9Waves = 9;
+typedef LeanLds<kLean9Waves> Lean9Lds;
+
+template <bool PACK>
+__global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLeanArgs A) {
+  extern __shared__ __align__(16) char lds[];
+  CLOCK_STAMP(A.c, 0);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t head = blockIdx.x;
+  lean_kernargs<KiviLeanArgs>();
+  char* qarea = lds + Lean9Lds::kBytes;
+  half8 qB[4];
+  char* slot = lds + Lean9Lds::kSlots + wave * kSlotBytes;
+  const int nwt = A.nwt;
+  WaveState st;
+  wave_state_init(st);
+  if (wave < 4 || wave == 8) {
+    // quantized: Q quarter w first (waves 0..3), then the group's loads
+    u32x4 qv = {0u, 0u, 0u, 0u};
+    if (wave < 4) qv = q_quarter_load(A.c, head, wave, lane);
+    QState qs;
+    q_state_init(qs);
+    const bool sk = wave == 8;
+    const bool has = sk || wave < nwt;
+    const QTensors T = sk ? q_sink_tensors(A.sinkq, head, A.sink)
+                          : q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
+    QTileRaw X;
+    load_q_group(T, sk ? 0u : head * (uint32_t)nwt + (uint32_t)wave, has, lane, X);
+    __syncthreads();
+    if (wave < 4) {
+      q_quarter_store(qarea, wave, lane, qv);
+      q_quarter_ready(qarea, lane);
+    }
+    q_operand_read<PACK>(qarea, lane, qB);
+    if (has)
+      q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * wave, sk ? A.sink : kTile, A.c.R,
+                               A.c.scale_log2, st, qs, lane);
+    lean_publish_ml<kLean9Waves>(A.c.G, st, lds, lane, wave);
+    publish_q<false, PACK, false>(qs, slot, lane);
+  } else {
+    // residual tile w - 4, its loads after the barrier (as in kivi_lean_kernel)
+    const int tile = wave - 4;
+    const int slot0 = A.sink + kTile * nwt + kTile * tile;
+    const rsrc_t rk = make_rsrc(A.kres, A.res_bytes), rv = make_rsrc(A.vres, A.res_bytes);
+    const uint32_t soff = head * (uint32_t)(A.res_rows * kRowBytes);
+    const bool has = tile * kTile < A.res_rows;
+    const uint32_t base = has && tile_any_valid(A.c.R, slot0) ? (uint32_t)tile * kSlotBytes : kOOB;
+    F16Raw X;
+    if (wave == 4 && lane == 0) *reinterpret_cast<int*>(qarea + kQAreaBytes) = 0;
+    __syncthreads();
+    if (has) load_f16(rk, rv, base, soff, lane, X);
+    q_operand_read<PACK>(qarea, lane, qB);
+    if (has) f16_tile_step(X, slot, qB, slot0, A.c.R, A.c.scale_log2, st, lane);
+    lean_publish_ml<kLean9Waves>(A.c.G, st, lds, lane, wave);
+    lean_publish_f(A.c.G, st, slot, lane);
+  }
+  // PACK: waves 0..3 and 8 left their rows unfolded
+  lean_merge<PACK ? 4 : 0, kLean9Waves, PACK>(A.c, lds, head);
 }
 
 // The fused KIVI decode past the lean kernel's windows (more than 7
@@ -1765,7 +1859,10 @@ int kivi_decode_t(const void* q, const void* k_res, const void* v_res, const voi
     A.nwt = S.nwt;
     A.sink = sink;
     SET_CLOCK(A.c);
-    if (lean)
+    if (lean && S.nwt == 4)
+      hipLaunchKernelGGL(kivi_lean9_kernel<PACK>, dim3((unsigned)P.pairs), dim3(64 * kLean9Waves),
+                         Lean9Lds::kBytes + kQLdsBytes, st, A);
+    else if (lean)
       hipLaunchKernelGGL(kivi_lean_kernel<PACK>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes + kQLdsBytes, st, A);
     else if constexpr (PACK)
       hipLaunchKernelGGL(kivi_wide_kernel<true>, dim3((unsigned)P.pairs), dim3(kWideThreads), kWideLdsBytes, st, A);

@@ -238,7 +238,8 @@ def test_quantized_attention_dominant_token(where, device):
     assert_nearly_rounded(o, ref)
 
 
-@pytest.mark.parametrize("W,L", [(384, L) for L in (1, 3, 4, 5, 60, 200, 300, 387, 388, 389)] +
+@pytest.mark.parametrize("W,L", [(256, L) for L in (1, 3, 4, 5, 60, 131, 200, 259, 260, 261)] +
+                         [(384, L) for L in (1, 3, 4, 5, 60, 200, 300, 387, 388, 389)] +
                          [(1024, L) for L in (3, 500, 900, 1027, 1028, 1029)])
 def test_quantized_attention_rampup(W, L, device):
     """Ramp-up (seq_len <= S + W): only the slots the _kv_indices rule marks
@@ -246,7 +247,8 @@ def test_quantized_attention_rampup(W, L, device):
     enough from N(0,1) data that a leak moves the output, small enough that
     the quantization groups they share with real tokens stay well conditioned
     (1e4, as in the fp16 sparse test, would swamp those groups' scales).
-    W = 384 runs the 8-wave kernel, W = 1024 the 16-wave one."""
+    W = 256 runs the 9-wave lean kernel (the sink group on its own wave),
+    W = 384 the 8-wave kernel, W = 1024 the 16-wave one."""
     from quant_kernel import build_quantized_kv_cache
     B, H, KVH, D = 2, 16, 2, 128
     kf = randn((B, KVH, max(L, 1), D), 30 + L)
@@ -345,7 +347,8 @@ def test_quantized_attention_rejects_small_window(device):
 @pytest.mark.parametrize("W", [256, 1024])
 def test_quantized_attention_sink_sizes(sink, W, device):
     """Sink groups of 1 to 32 real tokens (the API's sink argument): the
-    8-wave lean kernel (W=256), the 16-wave kernel (W=1024 with a sink of at
+    9-wave lean kernel (W=256, the sink group on wave 8: a half-group step
+    up to 16 tokens, a whole one above), the 16-wave kernel (W=1024 with a sink of at
     most 16 tokens: its half-group step after the loop) and the work-queue
     kernel (W=1024, sink > 16), in steady state and ramp-up."""
     from quant_kernel import build_quantized_kv_cache
@@ -368,7 +371,7 @@ def test_quantized_attention_sink_sizes(sink, W, device):
 @pytest.mark.parametrize("W", [256, 1024])
 def test_kivi_bit_identical_under_concurrent_load(W, device):
     """The fused decode's waves meet only at the Q readiness count (lean
-    kernel), the group-queue counter (16-wave kernel) and the merge barrier,
+    kernels), the group-queue counter (16-wave kernel) and the merge barrier,
     so a result must not depend on how far each wave has got.  Launches made
     while a second stream (default priority) copies 512 MiB through the same
     CUs and HBM must be bit-identical to a launch on an idle GPU (the lean
