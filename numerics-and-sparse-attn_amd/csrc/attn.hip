@@ -1033,10 +1033,10 @@ static_assert(LeanLds<kWaves>::kL == kLdsL && LeanLds<kWaves>::kSlots == kLdsSlo
               "the 8-wave lean layout is attn_kernel's");
 
 // Barrier, then one thread per (head, 4 channels) combines the NW waves'
-// published partials into the fp16 output rows of this KV head.  Waves
-// below NPACK, and the last wave when LASTPACK, published packed quantized
-// rows unfolded: their row hn + 8 (the remainder part) is added to row hn.
-template <int NPACK = 0, int NW = kWaves, bool LASTPACK = false>
+// published partials into the fp16 output rows of this KV head.  The waves
+// of bit mask PMASK published packed quantized rows unfolded: their row
+// hn + 8 (the remainder part) is added to row hn.
+template <unsigned PMASK = 0, int NW = kWaves>
 __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds, uint32_t head) {
   typedef LeanLds<NW> Lds;
   __syncthreads();
@@ -1053,15 +1053,14 @@ __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds,
     lw[w] = sh_l[w * kMaxGroup + hn];
     ow[w] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn, ch));
   }
-  constexpr int kRem = NPACK + (LASTPACK ? 1 : 0);
-  float4v orem[kRem > 0 ? kRem : 1];
+  float4v orem[NW];
 #pragma unroll
-  for (int i = 0; i < kRem; ++i) {
-    const int w = i < NPACK ? i : NW - 1;
-    orem[i] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn + 8, ch));
-  }
+  for (int w = 0; w < NW; ++w)
+    if ((PMASK >> w) & 1u)
+      orem[w] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn + 8, ch));
 #pragma unroll
-  for (int i = 0; i < kRem; ++i) ow[i < NPACK ? i : NW - 1] += orem[i];
+  for (int w = 0; w < NW; ++w)
+    if ((PMASK >> w) & 1u) ow[w] += orem[w];
   float M = mw[0];
 #pragma unroll
   for (int w = 1; w < NW; ++w) M = fmaxf(M, mw[w]);
@@ -1269,7 +1268,7 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     lean_publish_ml(A.c.G, st, lds, lane, wave);
     lean_publish_f(A.c.G, st, slot, lane);
   }
-  lean_merge<PACK ? 4 : 0>(A.c, lds, head);   // PACK: waves 0..3 left their rows unfolded
+  lean_merge<PACK ? 0xFu : 0u>(A.c, lds, head);   // PACK: waves 0..3 left their rows unfolded
 }
 
 // The lean KIVI kernel for exactly 4 window-old groups (W = 256 with
@@ -1340,7 +1339,340 @@ __global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLea
     lean_publish_f(A.c.G, st, slot, lane);
   }
   // PACK: waves 0..3 and 8 left their rows unfolded
-  lean_merge<PACK ? 4 : 0, kLean9Waves, PACK>(A.c, lds, head);
+  lean_merge<PACK ? 0x10Fu : 0u, kLean9Waves>(A.c, lds, head);
+}
+
+// The decode-time KIVI cache's decode over rings of 5 tiles (residual 128)
+// with at most 4 window-old groups, as a lean kernel of 10 waves: waves
+// 0..3 window-old slots 0..3, wave 8 the sink group, waves 4..7 and 9 ring
+// tiles 0..4.  MODE kRingOne: one ring state for every sequence (c.R);
+// kRingSeqs: per-sequence states ring[b] = {start, count}; kRingStep: one
+// token step per sequence first (kvdec_kivi_stream_step_decode), from the
+// sequence's count.  The three share the work split and the merge, so
+// step + decode and append followed by decode give bit-identical outputs.
+// kRingOne reads only the ring rows its state makes valid.  In the other
+// modes nothing waits on the state before the loads are issued: the ring
+// waves load their whole tiles, the state (the sink wave reads the count
+// after the first barrier and passes it on through LDS; kRingSeqs reads
+// ring[b]) decides only what is masked.  The ring tiles' loads follow the
+// workgroup barrier that the quantized waves reach once theirs are issued,
+// so the quantized groups (the long steps) get their data first.  The
+// step's memory operations are off the critical path:
+//   * the token's K/V row: every ring wave loads it from k_new / v_new
+//     before its tile, and the wave whose tile holds the row puts it in
+//     place of the ring's old content at its uses in the step (the tile's
+//     loads read the ring before the row is stored there) and, once its
+//     step is done, stores it into the ring for the later steps;
+//   * an eviction (every 32nd step of a sequence): the wave of the slot that
+//     receives the ring's oldest block quantizes it itself (the quantizers'
+//     exact group formulas), stores the group for the later steps and
+//     steps it from its LDS slot;
+//   * the bookkeeping: the sink wave takes the workgroup's arrival number
+//     once it has published its group; the last of the sequence's KVH
+//     workgroups to arrive records the step after the merge.
+// The general kernel (attn_kernel<KiviStepSrc>) read the count first, then
+// wrote the row and quantized an evicted block with every thread, then
+// passed a barrier before its first decode load, and took its arrival
+// number after its merge.
+enum { kRingOne = 0, kRingSeqs = 1, kRingStep = 2 };
+struct StepLeanArgs {
+  LeanCommon c;
+  const _Float16* k_new;   // [pairs][128]
+  const _Float16* v_new;
+  _Float16* k_ring;        // [pairs][cap][128]
+  _Float16* v_ring;
+  QRegion sinkq;           // [pairs] groups
+  QRegion winq;            // [pairs][nwg] groups (written on eviction)
+  int32_t* appended;       // [B] tokens appended since each sequence's prefill
+  const int32_t* active;   // [B] or null (all)
+  int32_t* arrive;         // [B] workgroups arrived this step (0 between launches)
+  int32_t* plan;           // [B][3] {row, evict block, evict slot} of this step
+  int32_t* ring;           // [B][2] kRingStep: {start, count} after this step; kRingSeqs: the states
+  uint32_t ring_bytes;     // pairs * cap * 256 (< 2^31)
+  uint32_t win_code_bytes, win_meta_bytes;
+  int nwg, sink, residual, cap, KVH;
+};
+constexpr int kStepWaves = 10;
+typedef LeanLds<kStepWaves> StepLds;
+
+// Quantize ring rows [32 blk, +32) of KV head `pair` into window-old slot
+// `slot` by one wave (the group formulas of evict_block, so the same
+// codes): lane L takes K channels 2L, 2L + 1 and V token L / 2, groups
+// 2 (L % 2) and 2 (L % 2) + 1.  The group is stored for the later steps;
+// its scales, zeros and V codes come back in X in the lane layout of a
+// loaded group, and its K code bytes go straight to the wave's LDS slot
+// (`stage_k`, called after the rest of the tile is staged).
+struct EvictK {
+  uint32_t rows[8];   // K code bytes of channels 2L, 2L + 1 for code rows 0..7
+};
+__device__ __forceinline__ void evict_group(const StepLeanArgs& A, uint32_t pair, int blk, int slot, int lane,
+                                            QTileRaw& X, EvictK& kb) {
+  const size_t row0 = (size_t)pair * A.cap + (size_t)blk * kTile;
+  const _Float16* kr = A.k_ring + row0 * kHeadDim;
+  const _Float16* vr = A.v_ring + row0 * kHeadDim;
+  const size_t g = (size_t)pair * A.nwg + slot;
+  // K: channels 2L, 2L + 1 over the block's 32 tokens
+  float x0[kTile], x1[kTile];
+#pragma unroll
+  for (int t = 0; t < kTile; ++t) {
+    const half2v h = *reinterpret_cast<const half2v*>(kr + (size_t)t * kHeadDim + 2 * lane);
+    x0[t] = (float)h[0];
+    x1[t] = (float)h[1];
+  }
+  QParams q0, q1;
+  const u32x2 c0 = quant_group(x0, q0), c1 = quant_group(x1, q1);
+  uint8_t* kp = const_cast<uint8_t*>(A.winq.kp) + g * (kTile / 4) * kHeadDim;
+#pragma unroll
+  for (int p = 0; p < kTile / 4; ++p) {
+    const uint32_t b0 = (c0[p >> 2] >> (8 * (p & 3))) & 0xffu, b1 = (c1[p >> 2] >> (8 * (p & 3))) & 0xffu;
+    kb.rows[p] = b0 | (b1 << 8);
+    *reinterpret_cast<uint16_t*>(kp + p * kHeadDim + 2 * lane) = (uint16_t)kb.rows[p];
+  }
+  const half2v ks = {(_Float16)q0.s, (_Float16)q1.s}, kz = {(_Float16)q0.z, (_Float16)q1.z};
+  X.ks = __builtin_bit_cast(uint32_t, ks);
+  X.kz = __builtin_bit_cast(uint32_t, kz);
+  *reinterpret_cast<uint32_t*>(const_cast<_Float16*>(A.winq.ks) + g * kHeadDim + 2 * lane) = X.ks;
+  *reinterpret_cast<uint32_t*>(const_cast<_Float16*>(A.winq.kz) + g * kHeadDim + 2 * lane) = X.kz;
+  // V: token t, channel groups g0, g0 + 1
+  const int t = lane >> 1, g0 = 2 * (lane & 1);
+  float y0[kTile], y1[kTile];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const half8 h = as_h8(*reinterpret_cast<const u32x4*>(vr + (size_t)t * kHeadDim + kTile * g0 + 8 * c));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) (c < 4 ? y0 : y1)[8 * (c & 3) + e] = (float)h[e];
+  }
+  QParams q2, q3;
+  const u32x2 c2 = quant_group(y0, q2), c3 = quant_group(y1, q3);
+  X.vc = u32x4{c2[0], c2[1], c3[0], c3[1]};
+  const size_t tok = g * kTile + t;
+  *reinterpret_cast<u32x4*>(const_cast<uint8_t*>(A.winq.vp) + tok * (kHeadDim / 4) + 8 * g0) = X.vc;
+  const half2v vs = {(_Float16)q2.s, (_Float16)q3.s}, vz = {(_Float16)q2.z, (_Float16)q3.z};
+  X.vs = __builtin_bit_cast(uint32_t, vs);
+  X.vz = __builtin_bit_cast(uint32_t, vz);
+  *reinterpret_cast<uint32_t*>(const_cast<_Float16*>(A.winq.vs) + tok * 4 + g0) = X.vs;
+  *reinterpret_cast<uint32_t*>(const_cast<_Float16*>(A.winq.vz) + tok * 4 + g0) = X.vz;
+}
+__device__ __forceinline__ void evict_stage_k(const EvictK& kb, char* slot, int lane) {
+#pragma unroll
+  for (int p = 0; p < kTile / 4; ++p)
+    *reinterpret_cast<uint16_t*>(slot + kQsK + p * kHeadDim + 2 * lane) = (uint16_t)kb.rows[p];
+}
+
+// f16_tile_step of a ring tile whose row rr (rr < 0: none) is replaced by
+// the token's row, chunk t of K and V in kn, vn of lane (t, g).  The row is
+// put in at its uses (K: written over the staged row in the wave's LDS slot;
+// V: selected in the PV operand), so the step still waits for the tile's
+// loads one at a time: replacing the registers up front would wait for all
+// of them first.
+__device__ __forceinline__ void ring_tile_step(const F16Raw& X, char* slot, const half8 (&qB)[4], int slot0,
+                                               const SlotRanges& R, float scale_log2, WaveState& st, int lane,
+                                               int rr, const u32x4& kn, const u32x4& vn) {
+  const uint32_t t = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    *reinterpret_cast<u32x4*>(slot + kslot_off(4u * i + g, t)) = X.k[i];
+  if (rr >= 0 && (int)g == (rr & 3)) *reinterpret_cast<u32x4*>(slot + kslot_off((uint32_t)rr, t)) = kn;
+  auto kop = [&](int blk, int c) {
+    return *reinterpret_cast<const u32x4*>(slot + kslot_off(16u * blk + t, 4u * c + g));
+  };
+  // V row rr is tau(gv, jv): X.v[jv] of the lanes g == gv
+  const int jv = rr >= 0 ? 4 * (rr >> 4) + (rr & 3) : -1;
+  const bool vl = rr >= 0 && (int)g == ((rr >> 2) & 3);
+  auto vrow = [&](int w, int j) { return j == jv && vl ? vn[w] : X.v[j][w]; };
+  const TileRows T{slot0, 4};
+  if (tile_fully_valid(R, T)) {
+    tile_body<true>(kop, vrow, 0u, qB, scale_log2, st, NoRescale());
+  } else {
+    const uint32_t valid = tile_valid_bits(R, T, kTile, lane);
+    tile_body<false>(kop, [&](int w, int j) { return ((valid >> j) & 1u) ? vrow(w, j) : 0u; }, valid, qB,
+                     scale_log2, st, NoRescale());
+  }
+}
+
+template <bool PACK, int MODE>
+__global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanArgs A) {
+  extern __shared__ __align__(16) char lds[];
+  CLOCK_STAMP(A.c, 0);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t pair = blockIdx.x;
+  lean_kernargs<StepLeanArgs>();
+  const uint32_t b = pair / (uint32_t)A.KVH;
+  char* qarea = lds + StepLds::kBytes;
+  // kRingStep: the sequence's count and activity, read from memory by the
+  // sink wave alone once the barrier below has passed (a scalar load in
+  // front of the barrier would hold every wave's loads back by its round
+  // trip) and passed to the other waves through LDS: (n << 1 | active) and
+  // a readiness flag, polled with a bound.  Since no other wave of the
+  // workgroup reads the count from memory, the sink wave may take the
+  // workgroup's arrival number at any point after it has it.
+  int* cnt_word = reinterpret_cast<int*>(qarea + kQAreaBytes + 4);
+  int* cnt_flag = reinterpret_cast<int*>(qarea + kQAreaBytes + 8);
+  auto count_from_lds = [&](int& n, bool& act) {
+    bool ready = false;
+    for (int it = 0; it < (1 << 16); ++it) {
+      if (__hip_atomic_load(cnt_flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) {
+        ready = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    const int v = ready ? *cnt_word : 0;   // (never runs out: the sink wave always publishes)
+    n = v >> 1;
+    act = (v & 1) != 0;
+  };
+  // kRingSeqs: the sequence's ring state, clamped (read after the barrier)
+  auto seq_state = [&]() {
+    const int s0 = min(max((int)((cint32*)A.ring)[2 * b], 0), A.cap - 1);
+    const int c0 = min(max((int)((cint32*)A.ring)[2 * b + 1], 0), A.cap);
+    return RingStep{-1, -1, -1, s0, c0};
+  };
+  half8 qB[4];
+  char* slot = lds + StepLds::kSlots + wave * kSlotBytes;
+  const int nwg = A.nwg;
+  WaveState st;
+  wave_state_init(st);
+  auto ranges = [&](const RingStep& rs) {
+    if constexpr (MODE == kRingOne) return A.c.R;
+    const int base = A.sink + kTile * nwg, end = rs.start + rs.count;
+    return end <= A.cap ? SlotRanges{base, base + rs.start, base + end}
+                        : SlotRanges{base + end - A.cap, base + rs.start, base + A.cap};
+  };
+  // kRingStep, the sink wave: its arrival number, and the step it took
+  int prev = 0, n = 0;
+  bool act = false;
+  RingStep rs = {};
+  if (wave < 4 || wave == 8) {
+    u32x4 qv = {0u, 0u, 0u, 0u};
+    if (wave < 4) qv = q_quarter_load(A.c, pair, wave, lane);
+    QState qs;
+    q_state_init(qs);
+    const bool sk = wave == 8;
+    const bool has = sk || wave < nwg;
+    const QTensors T = sk ? q_sink_tensors(A.sinkq, pair, A.sink)
+                          : q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
+    QTileRaw X;
+    load_q_group(T, sk ? 0u : pair * (uint32_t)nwg + (uint32_t)wave, has, lane, X);
+    __syncthreads();
+    if (MODE == kRingStep && sk) {
+      n = max((int)((cint32*)A.appended)[b], 0);
+      act = !A.active || ((cint32*)A.active)[b] != 0;
+      if (lane == 0) {
+        *cnt_word = n << 1 | (act ? 1 : 0);
+        __hip_atomic_store(cnt_flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    if (wave < 4) {
+      q_quarter_store(qarea, wave, lane, qv);
+      q_quarter_ready(qarea, lane);
+    }
+    q_operand_read<PACK>(qarea, lane, qB);
+    if constexpr (MODE == kRingStep) {
+      if (!sk) count_from_lds(n, act);
+      rs = ring_step(n, act, A.residual, A.cap, nwg);
+    } else if constexpr (MODE == kRingSeqs) {
+      rs = seq_state();
+    }
+    const SlotRanges R = ranges(rs);
+    if (has) {
+      if (MODE == kRingStep && !sk && rs.blk >= 0 && rs.slot == wave) {
+        // this slot receives the ring's oldest block this step
+        __builtin_amdgcn_s_waitcnt(0);   // the slot's old group has been read
+        EvictK kb;
+        evict_group(A, pair, rs.blk, rs.slot, lane, X, kb);
+        const float slack = q_tile_stage(X, slot, lane);
+        evict_stage_k(kb, slot, lane);
+        q_tile_consume<false, PACK>(slot, qB, A.sink + kTile * wave, kTile, R, A.c.scale_log2, slack, st, qs,
+                                    lane);
+      } else {
+        q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * wave, sk ? A.sink : kTile, R,
+                                 A.c.scale_log2, st, qs, lane);
+      }
+    }
+    lean_publish_ml<kStepWaves>(A.c.G, st, lds, lane, wave);
+    publish_q<false, PACK, false>(qs, slot, lane);
+    if (MODE == kRingStep && sk && lane == 0) {
+      // the workgroup's arrival, once the sink wave has published: a wait
+      // for the atomic's return waits for every memory operation the wave
+      // issued before it (the compiler's waits in the publish count the
+      // atomic too), and the return comes after the CU's loads in flight.
+      // The offset is a zero the compiler cannot prove uniform, so the
+      // atomic stays one lane's and its result is first needed at the end
+      // (a uniform-address atomic is rewritten to broadcast its result at
+      // once, waiting for the round trip there).
+      int zero;
+      asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+      prev = atomicAdd(A.arrive + b + zero, 1);
+    }
+  } else {
+    // ring tile r: rows 32 r .. 32 r + 31 of this head's ring, all of them
+    // loaded (the count decides which are valid), with the token's row
+    const int r = wave == 9 ? 4 : wave - 4;
+    const rsrc_t rk = make_rsrc(A.k_ring, A.ring_bytes), rv = make_rsrc(A.v_ring, A.ring_bytes);
+    const uint32_t soff = pair * (uint32_t)(A.cap * kRowBytes);
+    F16Raw X;
+    if (wave == 4 && lane == 0) {
+      *reinterpret_cast<int*>(qarea + kQAreaBytes) = 0;
+      *cnt_flag = 0;
+    }
+    const int t = lane & 15, g = lane >> 4;
+    u32x4 kn = {0u, 0u, 0u, 0u}, vn = {0u, 0u, 0u, 0u};
+    if (MODE == kRingStep) {
+      kn = *reinterpret_cast<const u32x4*>(A.k_new + (size_t)pair * kHeadDim + 8 * t);
+      vn = *reinterpret_cast<const u32x4*>(A.v_new + (size_t)pair * kHeadDim + 8 * t);
+    }
+    // the ring tile's loads follow the barrier that the quantized waves
+    // reach once theirs are issued (as in kivi_lean_kernel: their long
+    // steps get their data first).  kRingOne knows the ring state from its
+    // arguments and reads only the valid rows; the other modes learn it
+    // from memory and load the whole tile rather than wait for it.
+    __syncthreads();
+    if constexpr (MODE == kRingOne)
+      load_f16(rk, rv, (uint32_t)r * kSlotBytes, soff, A.c.R, A.sink + kTile * nwg + kTile * r, lane, X);
+    else
+      load_f16(rk, rv, (uint32_t)r * kSlotBytes, soff, lane, X);
+    q_operand_read<PACK>(qarea, lane, qB);
+    if constexpr (MODE == kRingStep) {
+      count_from_lds(n, act);
+      rs = ring_step(n, act, A.residual, A.cap, nwg);
+    } else if constexpr (MODE == kRingSeqs) {
+      rs = seq_state();
+    }
+    const SlotRanges R = ranges(rs);
+    // the token's row replaces the ring's old content of its tile row
+    const bool owner = MODE == kRingStep && rs.row >= 0 && rs.row / kTile == r;
+    if constexpr (MODE == kRingStep)
+      ring_tile_step(X, slot, qB, A.sink + kTile * nwg + kTile * r, R, A.c.scale_log2, st, lane,
+                     owner ? rs.row % kTile : -1, kn, vn);
+    else
+      f16_tile_step(X, slot, qB, A.sink + kTile * nwg + kTile * r, R, A.c.scale_log2, st, lane);
+    lean_publish_ml<kStepWaves>(A.c.G, st, lds, lane, wave);
+    lean_publish_f(A.c.G, st, slot, lane);
+    if (owner && g < 2) {
+      // and stored into the ring for the later steps (lanes g = 0 the K
+      // chunks, g = 1 the V chunks; no wave of this launch reads the row
+      // from memory: an evicted block never holds it).  After the step: a
+      // store in flight among the tile's loads makes the compiler wait for
+      // all of them, and the store, at the step's first use of the tile.
+      _Float16* dst = (g == 0 ? A.k_ring : A.v_ring) + ((size_t)pair * A.cap + rs.row) * kHeadDim + 8 * t;
+      *reinterpret_cast<u32x4*>(dst) = g == 0 ? kn : vn;
+    }
+  }
+  // PACK: waves 0..3 and 8 left their rows unfolded
+  lean_merge<PACK ? 0x10Fu : 0u, kStepWaves>(A.c, lds, pair);
+  // the step's record, by the last of the sequence's workgroups to arrive
+  // (after the merge: the arrival atomic's round trip does not hold the
+  // merge's barrier back)
+  if (MODE == kRingStep && wave == 8 && lane == 0 && prev == A.KVH - 1) {
+    A.arrive[b] = 0;
+    A.appended[b] = n + (act ? 1 : 0);
+    A.plan[3 * b] = rs.row;
+    A.plan[3 * b + 1] = rs.blk;
+    A.plan[3 * b + 2] = rs.blk >= 0 ? rs.slot : -1;
+    A.ring[2 * b] = rs.start;
+    A.ring[2 * b + 1] = rs.count;
+  }
 }
 
 // The fused KIVI decode past the lean kernel's windows (more than 7
@@ -1960,6 +2292,33 @@ int stream_decode_t(const void* q, const void* k_ring, const void* v_ring, const
   S.nwt = n_groups;
   S.lens = ring;
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  // the 10-wave ring kernel: a ring of 5 tiles, at most 4 window-old
+  // groups, every tensor small enough for 31-bit offsets
+  if (ring_cap == 5 * kTile && n_groups <= 4 && P.pairs * ring_cap * kRowBytes < ((int64_t)1 << 31) &&
+      P.pairs <= 0x7fffffffLL) {
+    StepLeanArgs L{};
+    L.c = lean_common(P);
+    L.k_ring = const_cast<_Float16*>(S.kres);
+    L.v_ring = const_cast<_Float16*>(S.vres);
+    L.sinkq = S.sinkq;
+    L.winq = S.winq;
+    L.ring = const_cast<int32_t*>(ring);
+    L.ring_bytes = (uint32_t)(P.pairs * ring_cap * kRowBytes);
+    L.win_code_bytes = (uint32_t)(P.pairs * n_groups * 1024);
+    L.win_meta_bytes = (uint32_t)(P.pairs * n_groups * 256);
+    L.nwg = n_groups;
+    L.sink = sink;
+    L.cap = ring_cap;
+    L.KVH = KVH;
+    SET_CLOCK(L.c);
+    if (ring)
+      hipLaunchKernelGGL((kivi_ring_kernel<PACK, kRingSeqs>), dim3((unsigned)P.pairs), dim3(64 * kStepWaves),
+                         StepLds::kBytes + kQLdsBytes, st, L);
+    else
+      hipLaunchKernelGGL((kivi_ring_kernel<PACK, kRingOne>), dim3((unsigned)P.pairs), dim3(64 * kStepWaves),
+                         StepLds::kBytes + kQLdsBytes, st, L);
+    return launch_status();
+  }
   if (ring) return launch_attn(P, S, true, 0, st);
   KiviSrc<PACK> S1{};
   S1.kres = S.kres;
@@ -2057,6 +2416,37 @@ int stream_step_decode_t(const void* q, const void* k_new, const void* v_new, vo
   a.nwg = n_groups;
   a.KVH = KVH;
   a.residual = residual;
+  // the 10-wave step kernel: a ring of 5 tiles, at most 4 window-old
+  // groups, every tensor small enough for 31-bit offsets
+  if (ring_cap == 5 * kTile && n_groups <= 4 && P.pairs * ring_cap * kRowBytes < ((int64_t)1 << 31) &&
+      P.pairs <= 0x7fffffffLL) {
+    StepLeanArgs L;
+    L.c = lean_common(P);
+    L.c.R = SlotRanges{0, 0, 0};
+    L.k_new = a.k_new;
+    L.v_new = a.v_new;
+    L.k_ring = a.k_ring;
+    L.v_ring = a.v_ring;
+    L.sinkq = S.sinkq;
+    L.winq = S.winq;
+    L.appended = appended;
+    L.active = active;
+    L.arrive = arrive;
+    L.plan = plan;
+    L.ring = ring;
+    L.ring_bytes = (uint32_t)(P.pairs * ring_cap * kRowBytes);
+    L.win_code_bytes = (uint32_t)(P.pairs * n_groups * 1024);
+    L.win_meta_bytes = (uint32_t)(P.pairs * n_groups * 256);
+    L.nwg = n_groups;
+    L.sink = sink;
+    L.residual = residual;
+    L.cap = ring_cap;
+    L.KVH = KVH;
+    SET_CLOCK(L.c);
+    hipLaunchKernelGGL((kivi_ring_kernel<PACK, kRingStep>), dim3((unsigned)P.pairs), dim3(64 * kStepWaves),
+                       StepLds::kBytes + kQLdsBytes, static_cast<hipStream_t>(stream), L);
+    return launch_status();
+  }
   return launch_attn(P, S, true, 0, static_cast<hipStream_t>(stream));
 }
 

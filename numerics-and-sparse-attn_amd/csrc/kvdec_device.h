@@ -364,6 +364,20 @@ __device__ __forceinline__ void load_f16(rsrc_t rk, rsrc_t rv, uint32_t base, ui
   for (int j = 0; j < 8; ++j) X.v[j] = bload16(rv, base + (uint32_t)tau(g, j) * kRowBytes + 16u * t, soff);
 }
 
+// The same, reading only the rows whose slots (slot0 + row) are valid in R:
+// the other rows' registers hold zeros and cost no memory access.
+__device__ __forceinline__ void load_f16(rsrc_t rk, rsrc_t rv, uint32_t base, uint32_t soff,
+                                         const SlotRanges& R, int slot0, int lane, F16Raw& X) {
+  const uint32_t t = lane & 15, g = lane >> 4;
+  auto off = [&](uint32_t row) {
+    return slot_valid(R, slot0 + (int)row) ? base + row * kRowBytes + 16u * t : kOOB;
+  };
+#pragma unroll
+  for (int i = 0; i < 8; ++i) X.k[i] = bload16(rk, off(4u * i + g), soff);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) X.v[j] = bload16(rv, off((uint32_t)tau(g, j)), soff);
+}
+
 // LDS byte offset of 16-byte chunk `chunk` of K row `row` inside a wave slot:
 // chunks are XOR-swizzled by the row so that both the row-wise stores and
 // the column-wise MFMA operand reads hit 16 distinct bank groups.
