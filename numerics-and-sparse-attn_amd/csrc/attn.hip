@@ -1035,10 +1035,12 @@ static_assert(LeanLds<kWaves>::kL == kLdsL && LeanLds<kWaves>::kSlots == kLdsSlo
 // Barrier, then one thread per (head, 4 channels) combines the NW waves'
 // published partials into the fp16 output rows of this KV head.  The waves
 // of bit mask PMASK published packed quantized rows unfolded: their row
-// hn + 8 (the remainder part) is added to row hn.
-template <unsigned PMASK = 0, int NW = kWaves>
+// hn + 8 (the remainder part) is added to row hn.  The waves of bit mask
+// SKIP (never wave 0) have had their partials combined into another's.
+template <unsigned PMASK = 0, int NW = kWaves, unsigned SKIP = 0>
 __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds, uint32_t head) {
   typedef LeanLds<NW> Lds;
+  static_assert((SKIP & 1u) == 0, "wave 0's partial is always read");
   __syncthreads();
   const float* sh_m = reinterpret_cast<const float*>(lds + Lds::kM);
   const float* sh_l = reinterpret_cast<const float*>(lds + Lds::kL);
@@ -1049,6 +1051,7 @@ __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds,
   float4v ow[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
+    if ((SKIP >> w) & 1u) continue;
     mw[w] = sh_m[w * kMaxGroup + hn];
     lw[w] = sh_l[w * kMaxGroup + hn];
     ow[w] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn, ch));
@@ -1063,11 +1066,13 @@ __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds,
     if ((PMASK >> w) & 1u) ow[w] += orem[w];
   float M = mw[0];
 #pragma unroll
-  for (int w = 1; w < NW; ++w) M = fmaxf(M, mw[w]);
+  for (int w = 1; w < NW; ++w)
+    if (!((SKIP >> w) & 1u)) M = fmaxf(M, mw[w]);
   float L = 0.f;
   float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
+    if ((SKIP >> w) & 1u) continue;
     const float f = __builtin_amdgcn_exp2f(mw[w] - M);
     L += lw[w] * f;
     acc += ow[w] * f;
@@ -1093,6 +1098,60 @@ __device__ __forceinline__ void lean_publish_f(int G, const WaveState& st, char*
   AttnCommon P{};
   P.G = G;
   publish_f(P, st, slot, lane);
+}
+
+// Waves 0..3 of a lean kernel whose quantized steps end well before its
+// fp16 steps combine their four published partials into wave 0's while the
+// other waves still step, so that the merge, on the critical path, reads
+// one partial for the four (lean_merge SKIP 0xE).  Each wave counts itself
+// in (`count`, zeroed before the workgroup's first barrier), waits for the
+// four (a bounded poll; should it run out, the output is NaN), then wave w
+// combines heads 2w, 2w + 1 (and 2w + 8, 2w + 9 when G > 8): one thread
+// per (head, 4 channels), packed remainder rows (PACK) folded in.  The
+// threads of a head sit in one wave, whose reads of the four partials are
+// issued before its writes into wave 0's.
+template <bool PACK, int NW>
+__device__ __forceinline__ void quad_premerge(int G, char* lds, int* count, int lane, int wave) {
+  typedef LeanLds<NW> Lds;
+  if (lane == 0) __hip_atomic_fetch_add(count, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  bool ready = false;
+  for (int it = 0; it < (1 << 16); ++it) {
+    if (__hip_atomic_load(count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= 4) {
+      ready = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  float* sh_m = reinterpret_cast<float*>(lds + Lds::kM);
+  float* sh_l = reinterpret_cast<float*>(lds + Lds::kL);
+  for (int e = wave * 64 + lane; e < G * 32; e += 256) {
+    const int hn = e >> 5, ch = e & 31;
+    float mw[4], lw[4];
+    float4v ow[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = sh_m[w * kMaxGroup + hn];
+      lw[w] = sh_l[w * kMaxGroup + hn];
+      ow[w] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn, ch));
+      if (PACK)
+        ow[w] += *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn + 8, ch));
+    }
+    float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+    float L = 0.f;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = __builtin_amdgcn_exp2f(mw[w] - M);
+      L += lw[w] * f;
+      acc += ow[w] * f;
+    }
+    if (!ready) M = __builtin_nanf("");
+    *reinterpret_cast<float4v*>(lds + Lds::kSlots + row_off(hn, ch)) = acc;
+    if (ch == 0) {
+      sh_m[hn] = M;
+      sh_l[hn] = L;
+    }
+  }
 }
 
 // fp16 rows [heads][rows][128] (the compacted sink + window cache, or a
@@ -1272,13 +1331,18 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
 }
 
 // The lean KIVI kernel for exactly 4 window-old groups (W = 256 with
-// R = 128) with a ninth wave: waves 0..3 step window-old group w, wave 8 the
-// sink group, waves 4..7 residual tiles 0..3.  In the 8-wave kernel the
+// R = 128) with a ninth wave: waves 0..3 step window-old group w, wave 4 the
+// sink group, waves 5..8 residual tiles 0..3.  In the 8-wave kernel the
 // fifth quantized item (the sink group) falls to wave 0, whose two steps in
 // series (each ~1.3 us for a single wave on its SIMD) end the kernel last;
-// here the sink step runs in its own wave beside them (wave 8 shares SIMD 0
-// with waves 0 and 4; 136 VGPRs fit three waves per SIMD).  Measured per
+// here the sink step runs in its own wave beside them (wave 4 shares SIMD 0
+// with waves 0 and 8; 138 VGPRs fit three waves per SIMD).  Measured per
 // step (interleaved A/B, two boxes): 5.78 -> 5.67 us and 5.79 -> 5.69 us.
+// The sink wave is wave 4 rather than the last one: waves start in order,
+// ~0.05 us apart, and the residual waves issue their loads only after the
+// barrier anyway, while the sink's step, sharing its SIMD with a window-old
+// group's, published last when it started last (5.63 -> 5.47 us, with the
+// four window-old partials combined early by quad_premerge).
 // With fewer window-old groups every quantized item already has a wave of
 // its own and the extra wave only costs (W = 160: 5.22 -> 5.43 us).
 constexpr int kLean9Waves = 9;
@@ -1293,18 +1357,19 @@ __global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLea
   const uint32_t head = blockIdx.x;
   lean_kernargs<KiviLeanArgs>();
   char* qarea = lds + Lean9Lds::kBytes;
+  int* premerge_count = reinterpret_cast<int*>(qarea + kQAreaBytes + 12);
   half8 qB[4];
   char* slot = lds + Lean9Lds::kSlots + wave * kSlotBytes;
   const int nwt = A.nwt;
   WaveState st;
   wave_state_init(st);
-  if (wave < 4 || wave == 8) {
+  if (wave <= 4) {
     // quantized: Q quarter w first (waves 0..3), then the group's loads
     u32x4 qv = {0u, 0u, 0u, 0u};
     if (wave < 4) qv = q_quarter_load(A.c, head, wave, lane);
     QState qs;
     q_state_init(qs);
-    const bool sk = wave == 8;
+    const bool sk = wave == 4;
     const bool has = sk || wave < nwt;
     const QTensors T = sk ? q_sink_tensors(A.sinkq, head, A.sink)
                           : q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
@@ -1321,16 +1386,20 @@ __global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLea
                                A.c.scale_log2, st, qs, lane);
     lean_publish_ml<kLean9Waves>(A.c.G, st, lds, lane, wave);
     publish_q<false, PACK, false>(qs, slot, lane);
+    if (wave < 4) quad_premerge<PACK, kLean9Waves>(A.c.G, lds, premerge_count, lane, wave);
   } else {
-    // residual tile w - 4, its loads after the barrier (as in kivi_lean_kernel)
-    const int tile = wave - 4;
+    // residual tile w - 5, its loads after the barrier (as in kivi_lean_kernel)
+    const int tile = wave - 5;
     const int slot0 = A.sink + kTile * nwt + kTile * tile;
     const rsrc_t rk = make_rsrc(A.kres, A.res_bytes), rv = make_rsrc(A.vres, A.res_bytes);
     const uint32_t soff = head * (uint32_t)(A.res_rows * kRowBytes);
     const bool has = tile * kTile < A.res_rows;
     const uint32_t base = has && tile_any_valid(A.c.R, slot0) ? (uint32_t)tile * kSlotBytes : kOOB;
     F16Raw X;
-    if (wave == 4 && lane == 0) *reinterpret_cast<int*>(qarea + kQAreaBytes) = 0;
+    if (wave == 5 && lane == 0) {
+      *reinterpret_cast<int*>(qarea + kQAreaBytes) = 0;
+      *premerge_count = 0;
+    }
     __syncthreads();
     if (has) load_f16(rk, rv, base, soff, lane, X);
     q_operand_read<PACK>(qarea, lane, qB);
@@ -1338,14 +1407,14 @@ __global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLea
     lean_publish_ml<kLean9Waves>(A.c.G, st, lds, lane, wave);
     lean_publish_f(A.c.G, st, slot, lane);
   }
-  // PACK: waves 0..3 and 8 left their rows unfolded
-  lean_merge<PACK ? 0x10Fu : 0u, kLean9Waves>(A.c, lds, head);
+  // waves 0..3 are in wave 0's partial; PACK: wave 4 left its rows unfolded
+  lean_merge<PACK ? 0x10u : 0u, kLean9Waves, 0xEu>(A.c, lds, head);
 }
 
 // The decode-time KIVI cache's decode over rings of 5 tiles (residual 128)
 // with at most 4 window-old groups, as a lean kernel of 10 waves: waves
-// 0..3 window-old slots 0..3, wave 8 the sink group, waves 4..7 and 9 ring
-// tiles 0..4.  MODE kRingOne: one ring state for every sequence (c.R);
+// 0..3 window-old slots 0..3, wave 4 the sink group (as in
+// kivi_lean9_kernel), waves 5..9 ring tiles 0..4.  MODE kRingOne: one ring state for every sequence (c.R);
 // kRingSeqs: per-sequence states ring[b] = {start, count}; kRingStep: one
 // token step per sequence first (kvdec_kivi_stream_step_decode), from the
 // sequence's count.  The three share the work split and the merge, so
@@ -1509,6 +1578,7 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
   // workgroup's arrival number at any point after it has it.
   int* cnt_word = reinterpret_cast<int*>(qarea + kQAreaBytes + 4);
   int* cnt_flag = reinterpret_cast<int*>(qarea + kQAreaBytes + 8);
+  int* premerge_count = reinterpret_cast<int*>(qarea + kQAreaBytes + 12);
   auto count_from_lds = [&](int& n, bool& act) {
     bool ready = false;
     for (int it = 0; it < (1 << 16); ++it) {
@@ -1543,12 +1613,12 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
   int prev = 0, n = 0;
   bool act = false;
   RingStep rs = {};
-  if (wave < 4 || wave == 8) {
+  if (wave <= 4) {
     u32x4 qv = {0u, 0u, 0u, 0u};
     if (wave < 4) qv = q_quarter_load(A.c, pair, wave, lane);
     QState qs;
     q_state_init(qs);
-    const bool sk = wave == 8;
+    const bool sk = wave == 4;
     const bool has = sk || wave < nwg;
     const QTensors T = sk ? q_sink_tensors(A.sinkq, pair, A.sink)
                           : q_tensors(A.winq, A.win_code_bytes, A.win_meta_bytes);
@@ -1592,6 +1662,7 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
     }
     lean_publish_ml<kStepWaves>(A.c.G, st, lds, lane, wave);
     publish_q<false, PACK, false>(qs, slot, lane);
+    if (wave < 4) quad_premerge<PACK, kStepWaves>(A.c.G, lds, premerge_count, lane, wave);
     if (MODE == kRingStep && sk && lane == 0) {
       // the workgroup's arrival, once the sink wave has published: a wait
       // for the atomic's return waits for every memory operation the wave
@@ -1608,13 +1679,14 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
   } else {
     // ring tile r: rows 32 r .. 32 r + 31 of this head's ring, all of them
     // loaded (the count decides which are valid), with the token's row
-    const int r = wave == 9 ? 4 : wave - 4;
+    const int r = wave - 5;
     const rsrc_t rk = make_rsrc(A.k_ring, A.ring_bytes), rv = make_rsrc(A.v_ring, A.ring_bytes);
     const uint32_t soff = pair * (uint32_t)(A.cap * kRowBytes);
     F16Raw X;
-    if (wave == 4 && lane == 0) {
+    if (wave == 5 && lane == 0) {
       *reinterpret_cast<int*>(qarea + kQAreaBytes) = 0;
       *cnt_flag = 0;
+      *premerge_count = 0;
     }
     const int t = lane & 15, g = lane >> 4;
     u32x4 kn = {0u, 0u, 0u, 0u}, vn = {0u, 0u, 0u, 0u};
@@ -1659,12 +1731,12 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
       *reinterpret_cast<u32x4*>(dst) = g == 0 ? kn : vn;
     }
   }
-  // PACK: waves 0..3 and 8 left their rows unfolded
-  lean_merge<PACK ? 0x10Fu : 0u, kStepWaves>(A.c, lds, pair);
+  // waves 0..3 are in wave 0's partial; PACK: wave 4 left its rows unfolded
+  lean_merge<PACK ? 0x10u : 0u, kStepWaves, 0xEu>(A.c, lds, pair);
   // the step's record, by the last of the sequence's workgroups to arrive
   // (after the merge: the arrival atomic's round trip does not hold the
   // merge's barrier back)
-  if (MODE == kRingStep && wave == 8 && lane == 0 && prev == A.KVH - 1) {
+  if (MODE == kRingStep && wave == 4 && lane == 0 && prev == A.KVH - 1) {
     A.arrive[b] = 0;
     A.appended[b] = n + (act ? 1 : 0);
     A.plan[3 * b] = rs.row;
