@@ -95,7 +95,9 @@ static_assert(kMaxGroup * kHeadDim * 4 <= kSlotBytes, "partial output must fit a
 // Everything a tile step needs besides the tile itself.
 struct StepCtx {
   half8 qB[4];
-  float scale_log2;
+  float scale_log2;     // logit factor of fp16 tiles
+  float q_scale_log2;   // and of quantized tiles, with their K-scale factor
+  uint32_t kmul;        // (fp16 pair 2^-e: Q's prescale, q_prescale_exp)
   SlotRanges R;
   char* lds;    // workgroup LDS base
   char* slot;   // this wave's slot
@@ -169,7 +171,7 @@ struct QItems {
   __device__ __forceinline__ void step(int i, const Raw& X, State& s, const StepCtx& c) const {
     const bool sk = i == n - 1;
     q_tile_step<MIXED, PACK>(X, c.slot, c.qB, sk ? 0 : sink + kTile * i, sk ? sink : kTile, c.R,
-                             c.scale_log2, s.st, s.qs, c.lane);
+                             c.q_scale_log2, s.st, s.qs, c.lane, c.kmul);
   }
 };
 
@@ -842,6 +844,12 @@ template <class Src>
 struct packs_q<Src, decltype((void)Src::kPackQ)> {
   static constexpr bool value = Src::kPackQ;
 };
+// Whether a source has quantized tiles (the KIVI sources declare their Q
+// layout), whose steps take the prescaled Q operand (q_prescale).
+template <class Src, class = void>
+struct has_qtiles : std::false_type {};
+template <class Src>
+struct has_qtiles<Src, decltype((void)Src::kPackQ)> : std::true_type {};
 
 template <class Src>
 __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) {
@@ -895,6 +903,15 @@ __global__ __launch_bounds__(kThreads, 1) void attn_kernel(AttnCommon P, Src S) 
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) c.qB[cc] = qB[cc];
     c.scale_log2 = P.scale_log2;
+    // quantized tiles: Q's power-of-two prescale joins their K scales (a
+    // prescaled copy of the operand would not fit the registers here)
+    c.q_scale_log2 = P.scale_log2;
+    c.kmul = kOnePk;
+    if constexpr (has_qtiles<Src>::value) {
+      const int e = q_prescale_exp(qB);
+      c.q_scale_log2 = scale_pow2(P.scale_log2, e);
+      c.kmul = pow2_neg_pk(e);
+    }
     c.R = P.R;
     c.lds = lds;
     c.slot = lds + kLdsSlots + wave * kSlotBytes;
@@ -1297,10 +1314,11 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     q_quarter_store(qarea, wave, lane, qv);
     q_quarter_ready(qarea, lane);
     q_operand_read<PACK>(qarea, lane, qB);
+    const float sl2 = q_prescale(qB, A.c.scale_log2);
     auto step = [&](int i, const QTileRaw& X) {
       const bool sk = i == nwt;
       q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * i, sk ? A.sink : kTile, A.c.R,
-                               A.c.scale_log2, st, qs, lane);
+                               sl2, st, qs, lane);
     };
     if (i0 < n_q) step(i0, X0);
     if (i1 < n_q) step(i1, X1);
@@ -1381,9 +1399,10 @@ __global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLea
       q_quarter_ready(qarea, lane);
     }
     q_operand_read<PACK>(qarea, lane, qB);
+    const float sl2 = q_prescale(qB, A.c.scale_log2);
     if (has)
       q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * wave, sk ? A.sink : kTile, A.c.R,
-                               A.c.scale_log2, st, qs, lane);
+                               sl2, st, qs, lane);
     lean_publish_ml<kLean9Waves>(A.c.G, st, lds, lane, wave);
     publish_q<false, PACK, false>(qs, slot, lane);
     if (wave < 4) quad_premerge<PACK, kLean9Waves>(A.c.G, lds, premerge_count, lane, wave);
@@ -1638,6 +1657,7 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
       q_quarter_ready(qarea, lane);
     }
     q_operand_read<PACK>(qarea, lane, qB);
+    const float sl2 = q_prescale(qB, A.c.scale_log2);
     if constexpr (MODE == kRingStep) {
       if (!sk) count_from_lds(n, act);
       rs = ring_step(n, act, A.residual, A.cap, nwg);
@@ -1653,11 +1673,11 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
         evict_group(A, pair, rs.blk, rs.slot, lane, X, kb);
         const float slack = q_tile_stage(X, slot, lane);
         evict_stage_k(kb, slot, lane);
-        q_tile_consume<false, PACK>(slot, qB, A.sink + kTile * wave, kTile, R, A.c.scale_log2, slack, st, qs,
+        q_tile_consume<false, PACK>(slot, qB, A.sink + kTile * wave, kTile, R, sl2, slack, st, qs,
                                     lane);
       } else {
         q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * wave, sk ? A.sink : kTile, R,
-                                 A.c.scale_log2, st, qs, lane);
+                                 sl2, st, qs, lane);
       }
     }
     lean_publish_ml<kStepWaves>(A.c.G, st, lds, lane, wave);
@@ -1834,6 +1854,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs
     i = grab(ctr, lane);
     load(i, X);
   }
+  // the quantized items' Q operand, prescaled once the wave's first group
+  // load is in flight (before it, the wait for Q would hold the load back)
+  const float sl2 = q_prescale(qB, A.c.scale_log2);
   WaveState st;   // the quantized items' max and sum (st.O stays zero)
   wave_state_init(st);
   QState qs;
@@ -1845,13 +1868,13 @@ __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs
     const float slack = q_tile_stage(X, slot, lane);
     const int nx = grab(ctr, lane);
     load(nx, X);
-    q_tile_body<false, false, PACK>(slot, qB, A.sink + kTile * i, kTile, A.c.R, A.c.scale_log2, slack, st, qs,
+    q_tile_body<false, false, PACK>(slot, qB, A.sink + kTile * i, kTile, A.c.R, sl2, slack, st, qs,
                                     lane);
     i = nx;
   }
   if (i == nwt) {
     const float slack = q_tile_stage(X, slot, lane);
-    q_tile_body<false, true, PACK>(slot, qB, 0, A.sink, A.c.R, A.c.scale_log2, slack, st, qs, lane);
+    q_tile_body<false, true, PACK>(slot, qB, 0, A.sink, A.c.R, sl2, slack, st, qs, lane);
   }
   wide_publish_ml(A.c.G, st, lds, lane, wave);
   publish_q<false, PACK, false>(qs, slot, lane);

@@ -622,6 +622,7 @@ __device__ __forceinline__ void q_state_fold(QState& qs) {
 constexpr int kQsK = 0, kQsKS = 1024, kQsKZ = 1280, kQsV = 1536, kQsVS = 2560, kQsVZ = 2816;
 constexpr int kQsBytes = 3072;
 constexpr uint32_t kNegPk = 0x80008000u;   // sign bits of an fp16 pair
+constexpr uint32_t kOnePk = 0x3C003C00u;   // fp16 pair (1, 1)
 
 __device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
   *reinterpret_cast<u32x4*>(slot + kQsK + 16 * lane) = X.kc;
@@ -677,6 +678,75 @@ __device__ __forceinline__ u32x2 fields2(u32x2 w, uint32_t sh) {
   return u32x2{(uint32_t)x & 0x03030303u, (uint32_t)(x >> 32) & 0x03030303u};
 }
 
+// |x| <= 2^(E - 15) (1 + m / 1024) for the fp16 bits x of exponent E and
+// mantissa m: the least el with |x| <= 2^el (for normal x).
+__device__ __forceinline__ int absmax_exp_raw(uint32_t x) {
+  return (int)(x >> 10) - 15 + ((x & 0x3FFu) != 0u ? 1 : 0);
+}
+// Power-of-two prescale of the Q operand for quantized tiles.  Their QK
+// forms the fp16 product q * scale of a query channel and a K channel's
+// scale, finite for every fp16 scale only while |q| <= 1 (|q| = 64 with a
+// K channel whose 32-token range is above ~3072 would give inf, and the
+// MFMA against code 0 NaN).  The products are taken as (q * 2^-e) * scale
+// with 2^e the least power of two at or above the KV head's largest |q|
+// (e = 0, no change, when that is at most 1), and the quantized tiles'
+// logit factor takes 2^e back.  The scaling is exact unless a scaled value
+// falls below the fp16 normal range (|q| < 2^(e - 14)).  e is the wave's
+// (every wave holds the KV head's whole Q), so it stays uniform.
+__device__ __forceinline__ int q_prescale_exp(const half8 (&qB)[4]) {
+  typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+  // |q| bits (unsigned order = the order of non-negative fp16), reduced
+  // pairwise in a tree (a serial chain would be 32 dependent steps)
+  u16x2 v[16];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const u32x4 u = as_u4(qB[c]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[4 * c + i] = __builtin_bit_cast(u16x2, u[i] & 0x7FFF7FFFu);
+  }
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i) v[i] = __builtin_elementwise_max(v[i], v[i + w]);
+  const int el = absmax_exp_raw(max(v[0][0], v[0][1]));
+  int e = 0;   // the wave's largest el (at most 16), by a search over ballots
+#pragma unroll
+  for (int b = 16; b >= 1; b >>= 1)
+    if (__ballot(el >= e + b)) e += b;
+  return min(e, 16);
+}
+// The fp16 pair (2^-e, 2^-e), 0 <= e <= 16.
+__device__ __forceinline__ uint32_t pow2_neg_pk(int e) {
+  const uint32_t h = e <= 14 ? (uint32_t)(15 - e) << 10 : 0x0200u >> (e - 15);
+  return h | h << 16;
+}
+// scale_log2 * 2^e, kept uniform.
+__device__ __forceinline__ float scale_pow2(float scale_log2, int e) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                       __builtin_bit_cast(int, __builtin_ldexpf(scale_log2, e))));
+}
+// The Q operand scaled in place by 2^-e; returns the logit factor of every
+// quantized tile stepped with it (fp16 tiles, whose products are fp32 and
+// cannot overflow, keep the unscaled operand).  The empty asm statements
+// keep the multiplies where they are written: called while the wave's tile
+// loads are in flight, they would otherwise sink past the loads' wait onto
+// the step's critical path.
+__device__ __forceinline__ float q_prescale_by(half8 (&qB)[4], int e, float scale_log2) {
+  const uint32_t h = pow2_neg_pk(e);
+  const half8 p = as_h8(u32x4{h, h, h, h});
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    qB[c] = qB[c] * p;
+    asm volatile("" : "+v"(qB[c]));
+  }
+  return scale_pow2(scale_log2, e);
+}
+// The same with e found from the operand itself (every wave holds the KV
+// head's whole Q).
+__device__ __forceinline__ float q_prescale(half8 (&qB)[4], float scale_log2) {
+  return q_prescale_by(qB, q_prescale_exp(qB), scale_log2);
+}
+
 // Consume one KIVI tile staged in the wave's LDS slot.
 //   QK: the codes are exact fp16 integers (A operand); the per-channel K
 //       scale goes to the Q side as q * scale = head + remainder, both fp16
@@ -714,14 +784,17 @@ constexpr float kSlackVScale = 128.0f;
 template <bool MIXED, bool HALF, bool PACK>
 __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[4], int slot0,
                                             int xlim, const SlotRanges& R, float scale_log2,
-                                            float slack, WaveState& st, QState& qs, int lane) {
+                                            float slack, WaveState& st, QState& qs, int lane,
+                                            uint32_t kmul = kOnePk) {
   const int t = lane & 15, g = lane >> 4;
   const uint32_t pm = PACK ? pack_lanes(lane) : 0u;
-  // scale and negated zero of the lane's K channels 32c + 8g .. +7
+  // scale and negated zero of the lane's K channels 32c + 8g .. +7; kmul
+  // (2^-e, for a Q operand not prescaled itself) joins the scale
   half8 ks[4], nz[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     ks[c] = *reinterpret_cast<const half8*>(slot + kQsKS + 2 * (32 * c + 8 * g));
+    if (kmul != kOnePk) ks[c] = ks[c] * as_h8(u32x4{kmul, kmul, kmul, kmul});
     nz[c] = *reinterpret_cast<const half8*>(slot + kQsKZ + 2 * (32 * c + 8 * g));
   }
 
@@ -791,7 +864,6 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
   u32x4 nBm = {0u, 0u, 0u, 0u}, prm = {0u, 0u, 0u, 0u};
   if (PACK) {
     const u32x4 pBu = as_u4(pB);
-    constexpr uint32_t kOnePk = 0x3C003C00u;   // fp16 pair (1, 1)
     const u32x4 pr = {fma_mix_pk_f16(pf[0], pf[1], kOnePk, pBu[0]), fma_mix_pk_f16(pf[2], pf[3], kOnePk, pBu[1]),
                       fma_mix_pk_f16(pf[4], pf[5], kOnePk, pBu[2]), fma_mix_pk_f16(pf[6], pf[7], kOnePk, pBu[3])};
     nBm = (pBu ^ kNegPk) & pm;
@@ -860,20 +932,21 @@ __device__ __forceinline__ float q_tile_stage(const QTileRaw& raw, char* slot, i
 template <bool MIXED, bool PACK = false>
 __device__ __forceinline__ void q_tile_consume(char* slot, const half8 (&qB)[4], int slot0, int xlim,
                                                const SlotRanges& R, float scale_log2, float slack,
-                                               WaveState& st, QState& qs, int lane) {
+                                               WaveState& st, QState& qs, int lane,
+                                               uint32_t kmul = kOnePk) {
   if (xlim <= kTile / 2)
-    q_tile_body<MIXED, true, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+    q_tile_body<MIXED, true, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane, kmul);
   else
-    q_tile_body<MIXED, false, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+    q_tile_body<MIXED, false, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane, kmul);
 }
 
 template <bool MIXED, bool PACK = false>
 __device__ __forceinline__ void q_tile_step(const QTileRaw& raw, char* slot,
                                             const half8 (&qB)[4], int slot0, int xlim,
                                             const SlotRanges& R, float scale_log2, WaveState& st,
-                                            QState& qs, int lane) {
+                                            QState& qs, int lane, uint32_t kmul = kOnePk) {
   const float slack = q_tile_stage(raw, slot, lane);
-  q_tile_consume<MIXED, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane);
+  q_tile_consume<MIXED, PACK>(slot, qB, slot0, xlim, R, scale_log2, slack, st, qs, lane, kmul);
 }
 
 }  // namespace kvdec

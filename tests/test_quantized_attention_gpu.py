@@ -213,6 +213,41 @@ def test_quantized_attention_large_k_offsets(W, device):
     assert_nearly_rounded(o, ref)
 
 
+@pytest.mark.parametrize("W,varlen", [(32, False), (256, False), (512, False), (1024, False),
+                                      (256, True), (1024, True)])
+def test_quantized_attention_q_times_k_scale_beyond_fp16(W, varlen, device):
+    """|q| = 64 on a K channel whose 32-token groups span 0..30000 (K scale
+    10000): the fp16 product q * scale (-640000) is beyond the fp16 range,
+    which the kernels' power-of-two Q prescale keeps finite.  The channel's
+    other tokens are 0 (code 0 exactly), the outlier tokens (one window-old,
+    one sink) get logits of about -2e6 and weight 0, so every output stays
+    an ordinary attention result within half an fp16 ulp of the fp64
+    oracle.  Covers the lean kernels (W=32, 256), the 16-wave kernel (W=512,
+    1024) and the general kernel (per-sequence lengths)."""
+    from quant_kernel import build_quantized_kv_cache
+    B, H, KVH, D = 2, 16, 2, 128
+    gen = torch.Generator(device=device).manual_seed(23 + W)
+    q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
+    q[..., 5] = -64.0
+    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device)
+    kc[..., 5] = 0.0
+    kc[:, :, 1, 5] = 30000.0                          # sink group
+    if W > R:
+        kc[:, :, S + 40, 5] = 30000.0                 # a window-old group
+    kc = kc.half()
+    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    say(f"kivi q * k_scale beyond fp16 W={W} varlen={varlen}")
+    cache = build_quantized_kv_cache(kc, vc)
+    hc = _host_cache(cache)
+    assert float(hc["k_sink_scale"][..., 5].astype(np.float32).max()) == 10000.0
+    L = 163840
+    o = _attend(q, cache, torch.full((B,), L, dtype=torch.int32, device=device) if varlen else L, W)
+    ref = O.quantized_attention(host(q), W - R, hc, SCALE)
+    assert np.isfinite(o).all()
+    assert max_abs(o, ref) < ATTN_TOL
+    assert_nearly_rounded(o, ref)
+
+
 @pytest.mark.parametrize("where", ["window_old", "sink", "residual"])
 def test_quantized_attention_dominant_token(where, device):
     """One token carries almost all of a head's softmax weight, so the output
