@@ -41,7 +41,7 @@ extern "C" {
 #define KVDEC_E_WINDOW (-7)      /* window / sink / residual combination       */
 #define KVDEC_E_SEQLEN (-8)      /* seq_len < 1                                */
 #define KVDEC_E_BITS (-9)        /* only 2-bit codes are implemented           */
-#define KVDEC_E_UNSUPPORTED (-10)/* valid but not implemented (group != 32 ...) */
+#define KVDEC_E_UNSUPPORTED (-10)/* valid but not implemented for this entry point */
 
 /* ---- element types --------------------------------------------------- */
 #define KVDEC_F16 0
@@ -78,9 +78,12 @@ size_t kvdec_workspace_bytes(int kind, int64_t B, int32_t H, int32_t KVH,
  * Dense causal GQA decode: one query token per (batch, head) against the
  * whole context.  Replaces dense_kernel.py:70-82 (dense_decode_attention)
  * and its kernel dense_kernel.py:21-67.
- *   q, o : [B, H, D] fp16        k, v : [B, KVH, L, D] fp16
+ *   q, o : [B, H, D] dtype        k, v : [B, KVH, L, D] dtype
  *   head h reads KV head h / (H / KVH); H / KVH <= 16; D == 128.
  *   o = softmax(q k^T * sm_scale) v, fp32 softmax and accumulation.
+ *   dtype KVDEC_F16 runs the MFMA kernels; KVDEC_BF16 and KVDEC_F32 (which
+ *   the reference kernel also loads, dense_kernel.py:37,48-49) a generic
+ *   kernel in fp32 arithmetic, output rounded once to dtype.
  */
 int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o,
                        int dtype, int64_t B, int32_t H, int32_t KVH, int64_t L,
@@ -105,9 +108,11 @@ int kvdec_dense_decode_noalloc(const void* q, const void* k, const void* v, void
 
 /*
  * StreamingLLM sink + window decode over a compacted [B, KVH, sink+window, D]
- * fp16 cache.  Replaces sparse_kernel.py:105-118 (sparse_decode_attention) and
+ * cache.  Replaces sparse_kernel.py:105-118 (sparse_decode_attention) and
  * sparse_kernel.py:67-102; slot validity follows _kv_indices
- * (sparse_kernel.py:15-46) for KVDEC_LAYOUT_LINEAR.
+ * (sparse_kernel.py:15-46) for KVDEC_LAYOUT_LINEAR.  q, o and the caches
+ * are all of dtype (KVDEC_F16: MFMA kernels; KVDEC_BF16 / KVDEC_F32: the
+ * generic fp32 kernel, as for kvdec_dense_decode).
  */
 int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
                         void* o, int dtype, int64_t B, int32_t H, int32_t KVH,
@@ -143,7 +148,7 @@ int kvdec_paged_decode(const void* q, const void* k_pages, const void* v_pages,
 /*
  * kvdec_sparse_decode with one seq_len per sequence (seq_lens [B] int32 on
  * the device, each >= 1; the reference passes one scalar,
- * sparse_kernel.py:105-118).  Same cache, layouts, masking rule per
+ * sparse_kernel.py:105-118).  Same cache, dtypes, layouts, masking rule per
  * sequence and workspace (kvdec_workspace_bytes(KVDEC_KIND_SPARSE, ...)).
  */
 int kvdec_sparse_decode_varlen(const void* q, const void* k_cache, const void* v_cache,
@@ -156,10 +161,13 @@ int kvdec_sparse_decode_varlen(const void* q, const void* k_cache, const void* v
  * KIVI per-channel quantization of K.  Replaces quant_kernel.py:106-126
  * (quantize_k_cache) and quant_kernel.py:44-103.
  *   x      : [B, KVH, N, D] of in_dtype (KVDEC_F32, KVDEC_F16 or KVDEC_BF16)
- *   packed : [B, KVH, N/4, D] u8, code of token 4p+j in bits 2j..2j+1
+ *   packed : [B, KVH, N/pf, D] u8 with pf = 8 / bits codes per byte: code of
+ *            token pf*p+j in bits j*bits .. j*bits + bits - 1
  *   scale, zero : [B, KVH, N/group, D] fp16
- *   N % group == 0, D even, group == 32, bits == 2.
- * Codes are bit-exact to the IEEE-float32 closed form.
+ *   1 <= bits <= 8, N % group == 0, group % pf == 0 (whole bytes per group).
+ *   bits == 2 with group == 32 (D even) is the fast path, anything else a
+ *   generic kernel.  QMAX = 2^bits - 1; codes are bit-exact to the
+ *   IEEE-float32 closed form s = (mx - mn) / QMAX, ... (quant_kernel.py:77-99).
  */
 int kvdec_quantize_k(const void* x, int in_dtype, void* packed_u8,
                      void* scale_f16, void* zero_f16, int64_t B, int32_t KVH,
@@ -169,9 +177,10 @@ int kvdec_quantize_k(const void* x, int in_dtype, void* packed_u8,
 /*
  * KIVI per-token quantization of V.  Replaces quant_kernel.py:193-214
  * (quantize_v_cache) and quant_kernel.py:129-190.
- *   packed : [B, KVH, N, D/4] u8, code of channel 4c+j in bits 2j..2j+1
+ *   packed : [B, KVH, N, D/pf] u8, code of channel pf*c+j in bits j*bits ..
  *   scale, zero : [B, KVH, N, D/group] fp16
- *   D % group == 0, group == 32, bits == 2.
+ *   1 <= bits <= 8, D % group == 0, group % pf == 0; bits == 2 with group
+ *   == 32 is the fast path.
  */
 int kvdec_quantize_v(const void* x, int in_dtype, void* packed_u8,
                      void* scale_f16, void* zero_f16, int64_t B, int32_t KVH,
@@ -198,6 +207,10 @@ int kvdec_quantize_v(const void* x, int in_dtype, void* packed_u8,
  *   Runs in one pass (one workgroup per KV head): ws / ws_bytes are
  *   accepted for interface stability and ignored (kvdec_workspace_bytes
  *   returns 0 for KVDEC_KIND_KIVI).
+ *   bits / group other than 2 / 32 (the tensors of kvdec_quantize_k / _v at
+ *   that width, /4 above reading /pf) run a generic kernel in fp32
+ *   arithmetic: 1 <= bits <= 8, D % group == 0, group % pf == 0,
+ *   (window - residual) % group == 0, 1 <= sink <= group, residual >= 1.
  */
 int kvdec_sparse_decode_kivi(const void* q, const void* k_res, const void* v_res,
                              const void* const* kivi, void* o, int64_t B,

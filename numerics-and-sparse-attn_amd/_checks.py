@@ -4,6 +4,10 @@ from __future__ import annotations
 
 import torch
 
+# dtypes of the attention entry points' q / k / v / o and their kvdec codes
+# (include/kvdec.h: KVDEC_F16, KVDEC_F32, KVDEC_BF16)
+ATTN_DTYPES = {torch.float16: 0, torch.float32: 1, torch.bfloat16: 2}
+
 
 def require_gpu_tensor(name: str, t, dtypes=(torch.float16,), ndim: int | None = None,
                        contiguous: bool = True) -> None:

@@ -30,6 +30,7 @@ ARCH = "gfx950"
 SOURCES = (
     ("attn.hip", []),
     ("quant.hip", ["-ffp-contract=off"]),
+    ("generic.hip", []),
 )
 CLOCK_LIB_PATH = os.path.join(HERE, "libkvdec_clock.so")
 # object name, source, extra flags; each library links the objects it names
@@ -37,10 +38,11 @@ OBJECTS = (
     ("attn", "attn.hip", []),
     ("attn_clock", "attn.hip", ["-DKVDEC_CLOCK"]),
     ("quant", "quant.hip", ["-ffp-contract=off"]),
+    ("generic", "generic.hip", []),
 )
 LIBRARIES = (
-    (LIB_PATH, ("attn", "quant")),
-    (CLOCK_LIB_PATH, ("attn_clock", "quant")),
+    (LIB_PATH, ("attn", "quant", "generic")),
+    (CLOCK_LIB_PATH, ("attn_clock", "quant", "generic")),
 )
 
 COMMON_FLAGS = [

@@ -21,6 +21,7 @@
 // fp16 tiles to other residual waves, balancing the SIMDs' VALU load.
 
 #include "kvdec_device.h"
+#include "generic.h"
 #include "kvdec_stream.h"
 #include "kvdec.h"
 
@@ -349,28 +350,6 @@ __device__ __forceinline__ void merge_out(const AttnCommon& P, char* lds, int64_
     }
   }
   CLOCK_STAMP(P, 1);
-}
-
-// Validity ranges of the [sink + window] cache at this length (the
-// _kv_indices rule for the linear layout), clamped into [0, sink + window].
-__host__ __device__ inline SlotRanges sparse_ranges(int64_t seq_len, int32_t window, int32_t sink,
-                                                   int32_t layout) {
-  const int64_t S = sink, W = window, n = S + W;
-  auto clamp = [n](int64_t v) { return (int)(v < 0 ? 0 : (v > n ? n : v)); };
-  SlotRanges R;
-  R.va = clamp(seq_len < S ? seq_len : S);
-  if (layout == KVDEC_LAYOUT_LINEAR) {
-    const int64_t lo = 2 * S + W - seq_len;
-    R.vb = clamp(lo > S ? lo : S);
-    R.vc = clamp(n);
-  } else {
-    int64_t nwin = seq_len - S;
-    if (nwin < 0) nwin = 0;
-    if (nwin > W) nwin = W;
-    R.vb = clamp(S);
-    R.vc = clamp(S + nwin);
-  }
-  return R;
 }
 
 // The fp16 queue of one unit: wave w takes items w and w + kWaves at launch
@@ -2198,7 +2177,7 @@ int scratch_address(void** out) {
 int check_dense(const void* q, const void* k, const void* v, void* o, int dtype, int64_t B,
                 int32_t H, int32_t KVH, int64_t L, int32_t D) {
   if (!q || !k || !v || !o) return KVDEC_E_NULL;
-  if (dtype != KVDEC_F16) return KVDEC_E_DTYPE;
+  if (dtype != KVDEC_F16 && dtype != KVDEC_F32 && dtype != KVDEC_BF16) return KVDEC_E_DTYPE;
   int rc = check_heads(B, H, KVH, D);
   if (rc) return rc;
   if (L < 1) return KVDEC_E_SEQLEN;
@@ -2318,10 +2297,39 @@ bool packed_group(int32_t H, int32_t KVH, int64_t window_old_groups) {
   return window_old_groups >= kPackMinGroups && KVH > 0 && H % KVH == 0 && H / KVH <= kPackGroup;
 }
 
+// Code widths and group sizes other than 2 / 32: the generic kernel, with
+// the reference's layout assumptions (whole bytes per group, channel groups
+// that divide the head dim).
+int kivi_decode_generic(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
+                        void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH,
+                        int64_t seq_len, int32_t window, int32_t sink, int32_t residual, int32_t group,
+                        int32_t bits, float sm_scale, void* stream) {
+  if (!q || !k_res || !v_res || !kivi || !o) return KVDEC_E_NULL;
+  if (bits < 1 || bits > 8) return KVDEC_E_BITS;
+  if (group < 1 || kHeadDim % group != 0 || group % (8 / bits) != 0) return KVDEC_E_GROUP;
+  int rc = check_heads(B, H, KVH, kHeadDim);
+  if (rc) return rc;
+  if (seq_len < 1) return KVDEC_E_SEQLEN;
+  if (sink < 1 || sink > group || residual < 1 || window < 1) return KVDEC_E_WINDOW;
+  const int32_t res_rows = window < residual ? window : residual;
+  const int32_t win_tok = window - res_rows;
+  if (win_tok % group != 0) return KVDEC_E_GROUP;
+  for (int i = 0; i < 6; ++i)
+    if (!kivi[i]) return KVDEC_E_NULL;
+  if (win_tok > 0)
+    for (int i = 6; i < 12; ++i)
+      if (!kivi[i]) return KVDEC_E_NULL;
+  return generic_kivi_decode(q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window, sink, res_rows,
+                             win_tok, group, bits, sm_scale, static_cast<hipStream_t>(stream));
+}
+
 int kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
                 void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH, int64_t seq_len,
                 int32_t window, int32_t sink, int32_t residual, int32_t group, int32_t bits,
                 float sm_scale, void* stream) {
+  if (bits != 2 || group != kQGroup)
+    return kivi_decode_generic(q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window, sink, residual,
+                               group, bits, sm_scale, stream);
   const int64_t res_rows = window < residual ? window : residual;
   if (packed_group(H, KVH, group > 0 ? (window - res_rows) / group : 0))
     return kivi_decode_t<true>(
@@ -2574,7 +2582,7 @@ const char* kvdec_strerror(int code) {
     case KVDEC_E_WORKSPACE: return "workspace missing or smaller than kvdec_workspace_bytes()";
     case KVDEC_E_WINDOW: return "unsupported window / sink / residual combination";
     case KVDEC_E_SEQLEN: return "seq_len must be >= 1";
-    case KVDEC_E_BITS: return "only 2-bit quantization is implemented";
+    case KVDEC_E_BITS: return "code width outside 1..8 bits, or not 2 bits where only 2-bit codes are implemented";
     case KVDEC_E_UNSUPPORTED: return "valid arguments, but not implemented";
     default: break;
   }
@@ -2618,6 +2626,10 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int
                        size_t ws_bytes, void* stream) {
   int rc = check_dense(q, k, v, o, dtype, B, H, KVH, L, D);
   if (rc) return rc;
+  if (dtype != KVDEC_F16)
+    return generic_rows_decode(q, k, v, o, dtype, B, H, KVH, L, SlotRanges{(int)L, 0, 0}, nullptr, false,
+                               0, 0, KVDEC_LAYOUT_LINEAR, sm_scale, ws, ws_bytes,
+                               static_cast<hipStream_t>(stream));
   AttnCommon P{};
   P.q = static_cast<const _Float16*>(q);
   P.o = static_cast<_Float16*>(o);
@@ -2687,7 +2699,7 @@ int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
                         int32_t window, int32_t sink, int32_t layout, float sm_scale, void* ws,
                         size_t ws_bytes, void* stream) {
   if (!q || !k_cache || !v_cache || !o) return KVDEC_E_NULL;
-  if (dtype != KVDEC_F16) return KVDEC_E_DTYPE;
+  if (dtype != KVDEC_F16 && dtype != KVDEC_F32 && dtype != KVDEC_BF16) return KVDEC_E_DTYPE;
   int rc = check_heads(B, H, KVH, kHeadDim);
   if (rc) return rc;
   if (seq_len < 1) return KVDEC_E_SEQLEN;
@@ -2696,6 +2708,10 @@ int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
   if (layout == KVDEC_LAYOUT_RING && window < 1) return KVDEC_E_WINDOW;
   const int64_t n = (int64_t)window + sink;
   if (n * kRowBytes >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;
+  if (dtype != KVDEC_F16)
+    return generic_rows_decode(q, k_cache, v_cache, o, dtype, B, H, KVH, n,
+                               sparse_ranges(seq_len, window, sink, layout), nullptr, true, window, sink,
+                               layout, sm_scale, ws, ws_bytes, static_cast<hipStream_t>(stream));
   AttnCommon P{};
   P.q = static_cast<const _Float16*>(q);
   P.o = static_cast<_Float16*>(o);
@@ -2767,7 +2783,7 @@ int kvdec_sparse_decode_varlen(const void* q, const void* k_cache, const void* v
                                int32_t KVH, int32_t window, int32_t sink, int32_t layout,
                                float sm_scale, void* ws, size_t ws_bytes, void* stream) {
   if (!q || !k_cache || !v_cache || !o || !seq_lens) return KVDEC_E_NULL;
-  if (dtype != KVDEC_F16) return KVDEC_E_DTYPE;
+  if (dtype != KVDEC_F16 && dtype != KVDEC_F32 && dtype != KVDEC_BF16) return KVDEC_E_DTYPE;
   int rc = check_heads(B, H, KVH, kHeadDim);
   if (rc) return rc;
   if (window < 0 || sink < 0 || (int64_t)window + sink < 1) return KVDEC_E_WINDOW;
@@ -2775,6 +2791,10 @@ int kvdec_sparse_decode_varlen(const void* q, const void* k_cache, const void* v
   if (layout == KVDEC_LAYOUT_RING && window < 1) return KVDEC_E_WINDOW;
   const int64_t n = (int64_t)window + sink;
   if (n >= ((int64_t)1 << 30)) return KVDEC_E_SHAPE;
+  if (dtype != KVDEC_F16)
+    return generic_rows_decode(q, k_cache, v_cache, o, dtype, B, H, KVH, n, SlotRanges{0, 0, 0}, seq_lens,
+                               true, window, sink, layout, sm_scale, ws, ws_bytes,
+                               static_cast<hipStream_t>(stream));
   AttnCommon P{};
   P.q = static_cast<const _Float16*>(q);
   P.o = static_cast<_Float16*>(o);

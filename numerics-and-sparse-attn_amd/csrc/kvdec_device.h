@@ -27,6 +27,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kvdec.h"
+
 namespace kvdec {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -162,6 +164,28 @@ struct SlotRanges {
 
 __device__ __forceinline__ bool slot_valid(const SlotRanges& R, int s) {
   return s < R.va || (s >= R.vb && s < R.vc);
+}
+
+// Validity ranges of the [sink + window] cache at this length (the
+// _kv_indices rule for the linear layout), clamped into [0, sink + window].
+__host__ __device__ inline SlotRanges sparse_ranges(int64_t seq_len, int32_t window, int32_t sink,
+                                                   int32_t layout) {
+  const int64_t S = sink, W = window, n = S + W;
+  auto clamp = [n](int64_t v) { return (int)(v < 0 ? 0 : (v > n ? n : v)); };
+  SlotRanges R;
+  R.va = clamp(seq_len < S ? seq_len : S);
+  if (layout == KVDEC_LAYOUT_LINEAR) {
+    const int64_t lo = 2 * S + W - seq_len;
+    R.vb = clamp(lo > S ? lo : S);
+    R.vc = clamp(n);
+  } else {
+    int64_t nwin = seq_len - S;
+    if (nwin < 0) nwin = 0;
+    if (nwin > W) nwin = W;
+    R.vb = clamp(S);
+    R.vc = clamp(S + nwin);
+  }
+  return R;
 }
 
 // The slots of a 32-token tile: tile row r (0..31) is slot

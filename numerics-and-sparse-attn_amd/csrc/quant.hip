@@ -330,6 +330,98 @@ __global__ __launch_bounds__(256) void quantize_v_kernel(const T* __restrict__ x
   }
 }
 
+// Any code width and group size (quant_kernel.py:44-126 and :129-214 with
+// BITS and GROUP_SIZE as parameters): QMAX = 2^bits - 1, 8 / bits codes per
+// byte at bits j * bits, LSB first.  One thread per (group, channel) of K or
+// (token, channel group) of V, reading its inputs twice (min / max, then the
+// codes); the 2-bit, 32-group kernels above are the fast path.  The
+// quotient is the HIP default fp32 division, correctly rounded like the
+// reference's IEEE division.
+template <typename T>
+__device__ __forceinline__ float gen_elem(const T* x, size_t i) {
+  if constexpr (std::is_same<T, uint16_t>::value) return __builtin_bit_cast(float, (uint32_t)x[i] << 16);
+  else return (float)x[i];
+}
+__device__ __forceinline__ void gen_params(float mn, float mx, float qmax, float& s, float& z) {
+#pragma clang fp contract(off)
+  s = (mx - mn) / qmax;
+  s = (s == 0.0f) ? 1.0f : s;
+  z = floorf(-mn / s + 0.5f);
+}
+__device__ __forceinline__ uint32_t gen_code(float x, float s, float z, float qmax) {
+#pragma clang fp contract(off)
+  const float c = floorf(x / s + 0.5f) + z;
+  return (uint32_t)fminf(fmaxf(c, 0.0f), qmax);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quantize_k_generic_kernel(const T* __restrict__ x,
+                                                                 uint8_t* __restrict__ packed,
+                                                                 _Float16* __restrict__ scale,
+                                                                 _Float16* __restrict__ zero,
+                                                                 int64_t n_units, int D, int group,
+                                                                 int bits) {
+  const int pf = 8 / bits;
+  const float qmax = (float)((1 << bits) - 1);
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < n_units;
+       u += (int64_t)gridDim.x * blockDim.x) {
+    // u = pg * D + ch; the group's rows start at row pg * group (every
+    // sequence is a whole number of groups), its packed rows at pg * group / pf
+    const int64_t pg = u / D;
+    const int ch = (int)(u - pg * D);
+    const T* xg = x + (size_t)pg * group * D + ch;
+    float mn = gen_elem(xg, 0), mx = mn;
+    for (int t = 1; t < group; ++t) {
+      const float v = gen_elem(xg, (size_t)t * D);
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
+    float s, z;
+    gen_params(mn, mx, qmax, s, z);
+    uint8_t* pk = packed + (size_t)pg * (group / pf) * D + ch;
+    for (int b = 0; b < group / pf; ++b) {
+      uint32_t byte = 0;
+      for (int j = 0; j < pf; ++j)
+        byte |= gen_code(gen_elem(xg, (size_t)(b * pf + j) * D), s, z, qmax) << (j * bits);
+      pk[(size_t)b * D] = (uint8_t)byte;
+    }
+    scale[u] = (_Float16)s;
+    zero[u] = (_Float16)z;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quantize_v_generic_kernel(const T* __restrict__ x,
+                                                                 uint8_t* __restrict__ packed,
+                                                                 _Float16* __restrict__ scale,
+                                                                 _Float16* __restrict__ zero,
+                                                                 int64_t n_units, int group, int bits) {
+  const int pf = 8 / bits;
+  const float qmax = (float)((1 << bits) - 1);
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < n_units;
+       u += (int64_t)gridDim.x * blockDim.x) {
+    // u = row * (D / group) + channel group: its inputs are x[u * group ..],
+    // its packed bytes packed[u * group / pf ..] (the row's groups in order)
+    const T* xg = x + (size_t)u * group;
+    float mn = gen_elem(xg, 0), mx = mn;
+    for (int c = 1; c < group; ++c) {
+      const float v = gen_elem(xg, c);
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
+    float s, z;
+    gen_params(mn, mx, qmax, s, z);
+    uint8_t* pk = packed + (size_t)u * (group / pf);
+    for (int b = 0; b < group / pf; ++b) {
+      uint32_t byte = 0;
+      for (int j = 0; j < pf; ++j) byte |= gen_code(gen_elem(xg, b * pf + j), s, z, qmax) << (j * bits);
+      pk[b] = (uint8_t)byte;
+    }
+    scale[u] = (_Float16)s;
+    zero[u] = (_Float16)z;
+  }
+}
+
 __global__ __launch_bounds__(256) void dequant_k_tile_kernel(
     const uint8_t* __restrict__ packed, const _Float16* __restrict__ scale,
     const _Float16* __restrict__ zero, float* __restrict__ out, int64_t tok_start,
@@ -519,11 +611,38 @@ unsigned grid_for(int64_t threads_needed, int block) {
 int check_quant_args(const void* x, int in_dtype, const void* p, const void* s, const void* z,
                      int64_t B, int32_t KVH, int64_t N, int32_t D, int32_t group, int32_t bits) {
   if (!x || !p || !s || !z) return KVDEC_E_NULL;
-  if (bits != 2) return KVDEC_E_BITS;
+  if (bits < 1 || bits > 8) return KVDEC_E_BITS;
   if (in_dtype != KVDEC_F32 && in_dtype != KVDEC_F16 && in_dtype != KVDEC_BF16) return KVDEC_E_DTYPE;
   if (B < 1 || KVH < 1 || N < 1 || D < 1) return KVDEC_E_SHAPE;
   if (group < 1) return KVDEC_E_SHAPE;
   return KVDEC_OK;
+}
+
+template <typename T>
+void launch_quant_generic_t(bool k, const void* x, uint8_t* p, _Float16* s, _Float16* z, int64_t n_units,
+                            int D, int group, int bits, hipStream_t st) {
+  const unsigned grid = grid_for(n_units, 256);
+  if (k)
+    hipLaunchKernelGGL(quantize_k_generic_kernel<T>, dim3(grid), dim3(256), 0, st, static_cast<const T*>(x), p,
+                       s, z, n_units, D, group, bits);
+  else
+    hipLaunchKernelGGL(quantize_v_generic_kernel<T>, dim3(grid), dim3(256), 0, st, static_cast<const T*>(x), p,
+                       s, z, n_units, group, bits);
+}
+
+int launch_quant_generic(bool k, const void* x, int in_dtype, void* packed_u8, void* scale_f16,
+                         void* zero_f16, int64_t n_units, int D, int group, int bits, void* stream) {
+  auto* p = static_cast<uint8_t*>(packed_u8);
+  auto* s = static_cast<_Float16*>(scale_f16);
+  auto* z = static_cast<_Float16*>(zero_f16);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (in_dtype == KVDEC_F32)
+    launch_quant_generic_t<float>(k, x, p, s, z, n_units, D, group, bits, st);
+  else if (in_dtype == KVDEC_F16)
+    launch_quant_generic_t<_Float16>(k, x, p, s, z, n_units, D, group, bits, st);
+  else
+    launch_quant_generic_t<uint16_t>(k, x, p, s, z, n_units, D, group, bits, st);
+  return launch_status();
 }
 
 }  // namespace
@@ -536,7 +655,13 @@ int kvdec_quantize_k(const void* x, int in_dtype, void* packed_u8, void* scale_f
   int rc = check_quant_args(x, in_dtype, packed_u8, scale_f16, zero_f16, B, KVH, N, D, group, bits);
   if (rc) return rc;
   if (N % group != 0) return KVDEC_E_GROUP;
-  if (group != kGroup) return KVDEC_E_UNSUPPORTED;
+  if (bits != 2 || group != kGroup) {
+    // any width: whole bytes per group
+    if (group % (8 / bits) != 0) return KVDEC_E_GROUP;
+    const int64_t n_units = B * KVH * (N / group) * D;
+    return launch_quant_generic(true, x, in_dtype, packed_u8, scale_f16, zero_f16, n_units, D, group,
+                                bits, stream);
+  }
   if (D % 2 != 0) return KVDEC_E_SHAPE;
   if ((int64_t)D * kGroup * 4 >= ((int64_t)1 << 31)) return KVDEC_E_SHAPE;   // 32-bit buffer offsets
   const int64_t pairs = B * KVH;
@@ -566,7 +691,12 @@ int kvdec_quantize_v(const void* x, int in_dtype, void* packed_u8, void* scale_f
   int rc = check_quant_args(x, in_dtype, packed_u8, scale_f16, zero_f16, B, KVH, N, D, group, bits);
   if (rc) return rc;
   if (D % group != 0) return KVDEC_E_DGROUP;
-  if (group != kGroup) return KVDEC_E_UNSUPPORTED;
+  if (bits != 2 || group != kGroup) {
+    if (group % (8 / bits) != 0) return KVDEC_E_DGROUP;
+    const int64_t n_units = B * KVH * N * (D / group);
+    return launch_quant_generic(false, x, in_dtype, packed_u8, scale_f16, zero_f16, n_units, D, group,
+                                bits, stream);
+  }
   const int64_t n_units = B * KVH * N * (D / kGroup);
   const unsigned grid = grid_for(n_units, 256);
   hipStream_t st = static_cast<hipStream_t>(stream);

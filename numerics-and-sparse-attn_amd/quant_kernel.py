@@ -11,7 +11,10 @@ reach through Triton debug kernels.
 
 Codes, scales and zeros are bit-exact to the IEEE-float32 closed form of the
 reference's formulas (s = (mx - mn) / 3, s := 1 if 0, z = floor(-mn / s + 0.5),
-code = clamp(floor(x / s + 0.5) + z, 0, 3)).
+code = clamp(floor(x / s + 0.5) + z, 0, 3)).  The quantizers and the fused
+decode also take the reference's ``bits`` (1..8, QMAX = 2^bits - 1, 8 // bits
+codes per byte) and ``group_size`` parameters; widths and groups other than
+2 / 32 run generic kernels (the 2-bit, 32-group kernels are the fast path).
 """
 
 import torch
@@ -164,6 +167,10 @@ def sparse_decode_attention_quantized(
     build_quantized_kv_cache returns then) and there is no window-old part.
     ``seq_len`` may also be a [BATCH] int32 tensor on the GPU: each sequence
     is masked at its own length (ramp-up per sequence).
+    ``bits`` / ``group_size`` other than 2 / 32 (caches from
+    quantize_k_cache / quantize_v_cache with the same arguments, the sink
+    padded to one group) take the generic fp32 kernel: 1..8-bit codes,
+    8 // bits per byte, groups that divide D_HEAD and hold whole bytes.
     """
     tensors = dict(zip(_KIVI_ORDER, (k_sink_packed, k_sink_scale, k_sink_zero,
                                      v_sink_packed, v_sink_scale, v_sink_zero,
@@ -184,16 +191,21 @@ def sparse_decode_attention_quantized(
         raise ValueError(f"window ({window}) must be >= 1")
     res_rows = min(window, R)
     win_tok = window - res_rows
-    G = group_size
+    G, bits = int(group_size), int(bits)
+    if not 1 <= bits <= 8:
+        raise ValueError(f"bits must be in 1..8, got {bits}")
+    if G < 1 or D % G or G % (8 // bits):
+        raise ValueError(f"group_size {G} must divide D_HEAD ({D}) and hold whole bytes of {bits}-bit codes")
+    pf = 8 // bits
     _checks.require_shape("k_cache", k_cache, (B, KVH, res_rows, D))
     _checks.require_shape("v_cache", v_cache, (B, KVH, res_rows, D))
     expect = {
-        "k_sink_packed": (B, KVH, G // 4, D), "k_sink_scale": (B, KVH, 1, D), "k_sink_zero": (B, KVH, 1, D),
-        "v_sink_packed": (B, KVH, G, D // 4), "v_sink_scale": (B, KVH, G, D // G),
+        "k_sink_packed": (B, KVH, G // pf, D), "k_sink_scale": (B, KVH, 1, D), "k_sink_zero": (B, KVH, 1, D),
+        "v_sink_packed": (B, KVH, G, D // pf), "v_sink_scale": (B, KVH, G, D // G),
         "v_sink_zero": (B, KVH, G, D // G),
-        "k_win_packed": (B, KVH, win_tok // 4, D), "k_win_scale": (B, KVH, win_tok // G, D),
+        "k_win_packed": (B, KVH, win_tok // pf, D), "k_win_scale": (B, KVH, win_tok // G, D),
         "k_win_zero": (B, KVH, win_tok // G, D),
-        "v_win_packed": (B, KVH, win_tok, D // 4), "v_win_scale": (B, KVH, win_tok, D // G),
+        "v_win_packed": (B, KVH, win_tok, D // pf), "v_win_scale": (B, KVH, win_tok, D // G),
         "v_win_zero": (B, KVH, win_tok, D // G),
     }
     for name, t in tensors.items():

@@ -23,13 +23,15 @@ def sparse_decode_attention(q, k_cache, v_cache, seq_len, window, sink=SINK_SIZE
     """k_cache/v_cache must be [BATCH, N_KV_HEADS, SINK+WINDOW, D_HEAD].
 
     Mirrors sparse_kernel.py:105-118 (same arguments and defaults; ``layout``
-    is an added keyword).  fp16, contiguous, D_HEAD == 128.  ``seq_len`` may
-    also be a [BATCH] int32 tensor on the GPU: each sequence is masked at
-    its own length (each >= 1).
+    is an added keyword).  Contiguous, D_HEAD == 128; q and the caches share
+    one dtype: fp16 runs the MFMA kernels, bf16 and fp32 the generic fp32
+    kernel.  ``seq_len`` may also be a [BATCH] int32 tensor on the GPU: each
+    sequence is masked at its own length (each >= 1).
     """
-    _checks.require_gpu_tensor("q", q, ndim=3)
-    _checks.require_gpu_tensor("k_cache", k_cache, ndim=4)
-    _checks.require_gpu_tensor("v_cache", v_cache, ndim=4)
+    _checks.require_gpu_tensor("q", q, dtypes=tuple(_checks.ATTN_DTYPES), ndim=3)
+    _checks.require_gpu_tensor("k_cache", k_cache, dtypes=(q.dtype,), ndim=4)
+    _checks.require_gpu_tensor("v_cache", v_cache, dtypes=(q.dtype,), ndim=4)
+    dtype = _checks.ATTN_DTYPES[q.dtype]
     _checks.require_same_device(("q", q), ("k_cache", k_cache), ("v_cache", v_cache))
     if layout not in _LAYOUTS:
         raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {layout!r}")
@@ -51,12 +53,12 @@ def sparse_decode_attention(q, k_cache, v_cache, seq_len, window, sink=SINK_SIZE
     ws, nbytes = K.workspace(K.KIND_SPARSE, B, H, KVH, sink + window, D, q.device)
     if varlen:
         rc = K.lib.kvdec_sparse_decode_varlen(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), K.ptr(o),
-                                              K.ptr(seq_len), K.F16, B, H, KVH, window, sink,
+                                              K.ptr(seq_len), dtype, B, H, KVH, window, sink,
                                               _LAYOUTS[layout], float(sm_scale), K.ptr(ws), nbytes,
                                               K.stream_of(q))
         K.check(rc, "sparse_decode_attention")
         return o
-    rc = K.lib.kvdec_sparse_decode(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), K.ptr(o), K.F16, B, H,
+    rc = K.lib.kvdec_sparse_decode(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), K.ptr(o), dtype, B, H,
                                    KVH, seq_len, window, sink, _LAYOUTS[layout], float(sm_scale),
                                    K.ptr(ws), nbytes, K.stream_of(q))
     K.check(rc, "sparse_decode_attention")

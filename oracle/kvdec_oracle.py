@@ -1,7 +1,8 @@
 """CPU oracle for the decode-attention path.  TEST INFRASTRUCTURE ONLY.
 
 This module restates, in numpy, the reference's algorithms for dense GQA
-decode, StreamingLLM sink+window decode, the KIVI 2-bit quantizers, the tile
+decode, StreamingLLM sink+window decode, the KIVI quantizers (2-bit and any
+other code width the reference's BITS parameter allows), the tile
 dequantizers, the quantized-cache builder and the fused quantized decode.  It
 is the checker the HIP path is compared against.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
@@ -23,9 +24,10 @@ Conventions
   already rounded to the dtype the kernel sees (fp16), so the only differences
   left against the GPU are the GPU's own rounding.
 * Quantizer math is IEEE float32 with round-to-nearest-even, exactly as the
-  reference writes it: ``s = (mx - mn) / 3``, ``s = 1 if s == 0``,
-  ``z = floor(-mn / s + 0.5)``, ``code = clamp(floor(x / s + 0.5) + z, 0, 3)``
-  with the float32 ``s, z``; scale and zero are stored as fp16 (RNE).
+  reference writes it: ``s = (mx - mn) / QMAX``, ``s = 1 if s == 0``,
+  ``z = floor(-mn / s + 0.5)``, ``code = clamp(floor(x / s + 0.5) + z, 0, QMAX)``
+  with the float32 ``s, z`` and QMAX = 2^bits - 1 (3 for the default 2
+  bits); scale and zero are stored as fp16 (RNE).
 """
 
 from __future__ import annotations
@@ -253,18 +255,38 @@ def paged_attention(q, k_pages, v_pages, block_table, seq_lens, sm_scale, layout
 # KIVI 2-bit quantizers
 # --------------------------------------------------------------------------
 
-def _quant_params(mn, mx):
+def _quant_params(mn, mx, qmax=QMAX):
     """float32 scale / zero-point of one group, quant_kernel.py:79-81 (:168-170)."""
-    s = (mx - mn) / F32(QMAX)
+    s = (mx - mn) / F32(qmax)
     s = np.where(s == F32(0), F32(1), s).astype(F32)
     z = np.floor(-mn / s + F32(0.5)).astype(F32)
     return s, z
 
 
-def _codes(x, s, z):
-    """clamp(floor(x / s + 0.5) + z, 0, 3), quant_kernel.py:98-99 (:184-185)."""
+def _codes(x, s, z, qmax=QMAX):
+    """clamp(floor(x / s + 0.5) + z, 0, QMAX), quant_kernel.py:98-99 (:184-185)."""
     c = np.floor(x / s + F32(0.5)) + z
-    return np.minimum(np.maximum(c, F32(0)), F32(QMAX)).astype(np.uint8)
+    return np.minimum(np.maximum(c, F32(0)), F32(qmax)).astype(np.uint8)
+
+
+def _width(group_size, bits):
+    """QMAX and codes per byte of a ``bits``-wide code (quant_kernel.py:58-59,
+    :144-145), with the reference's layout assumption of whole bytes per group."""
+    if not 1 <= bits <= 8:
+        raise ValueError("bits must be in 1..8")
+    pf = 8 // bits
+    if group_size % pf:
+        raise ValueError("group_size must be a multiple of 8 // bits")
+    return (1 << bits) - 1, pf
+
+
+def _pack(codes, axis, pf, bits):
+    """packed[.., p, ..] = sum_j code[.., pf p + j, ..] << (j bits) along ``axis``
+    (quant_kernel.py:92-103, :176-190)."""
+    out = np.zeros(np.take(codes, np.arange(0, codes.shape[axis], pf), axis=axis).shape, dtype=np.int32)
+    for j in range(pf):
+        out |= np.take(codes, np.arange(j, codes.shape[axis], pf), axis=axis).astype(np.int32) << (j * bits)
+    return out.astype(np.uint8)
 
 
 def quantize_k(x, group_size=32, bits=2):
@@ -273,12 +295,11 @@ def quantize_k(x, group_size=32, bits=2):
     Restates quant_kernel.py:58-103 / :106-126.  x: [B, KVH, N, D] (any float
     dtype; converted to float32 exactly as ``.float()`` does).  Each group of
     ``group_size`` consecutive tokens gets, per channel, a float32 scale and
-    zero-point; codes are packed four per byte along tokens, LSB first:
-    packed[b,h,p,d] = sum_j code[b,h,4p+j,d] << 2j.
-    Returns (packed u8 [B,KVH,N/4,D], scale f16 [B,KVH,N/G,D], zero f16).
+    zero-point; codes are packed pf = 8 // bits per byte along tokens, LSB
+    first: packed[b,h,p,d] = sum_j code[b,h,pf p+j,d] << (j bits).
+    Returns (packed u8 [B,KVH,N/pf,D], scale f16 [B,KVH,N/G,D], zero f16).
     """
-    if bits != 2:
-        raise ValueError("only 2-bit quantization is defined")
+    qmax, pf = _width(group_size, bits)
     x = np.asarray(x).astype(F32)
     B, KVH, N, D = x.shape
     if N % group_size:
@@ -286,23 +307,20 @@ def quantize_k(x, group_size=32, bits=2):
     xg = x.reshape(B, KVH, N // group_size, group_size, D)
     mn = xg.min(axis=3)
     mx = xg.max(axis=3)
-    s, z = _quant_params(mn, mx)
-    codes = _codes(xg, s[:, :, :, None, :], z[:, :, :, None, :]).reshape(B, KVH, N, D)
-    packed = (codes[:, :, 0::4] | (codes[:, :, 1::4] << 2) | (codes[:, :, 2::4] << 4)
-              | (codes[:, :, 3::4] << 6)).astype(np.uint8)
-    return packed, s.astype(F16), z.astype(F16)
+    s, z = _quant_params(mn, mx, qmax)
+    codes = _codes(xg, s[:, :, :, None, :], z[:, :, :, None, :], qmax).reshape(B, KVH, N, D)
+    return _pack(codes, 2, pf, bits), s.astype(F16), z.astype(F16)
 
 
 def quantize_v(x, group_size=32, bits=2):
     """Per-token KIVI quantization of V.
 
     Restates quant_kernel.py:144-190 / :193-214: groups of ``group_size``
-    consecutive channels of one token; codes packed four per byte along
-    channels, LSB first: packed[b,h,t,c] = sum_j code[b,h,t,4c+j] << 2j.
-    Returns (packed u8 [B,KVH,N,D/4], scale f16 [B,KVH,N,D/G], zero f16).
+    consecutive channels of one token; codes packed pf = 8 // bits per byte
+    along channels, LSB first: packed[b,h,t,c] = sum_j code[b,h,t,pf c+j] << (j bits).
+    Returns (packed u8 [B,KVH,N,D/pf], scale f16 [B,KVH,N,D/G], zero f16).
     """
-    if bits != 2:
-        raise ValueError("only 2-bit quantization is defined")
+    qmax, pf = _width(group_size, bits)
     x = np.asarray(x).astype(F32)
     B, KVH, N, D = x.shape
     if D % group_size:
@@ -310,11 +328,9 @@ def quantize_v(x, group_size=32, bits=2):
     xg = x.reshape(B, KVH, N, D // group_size, group_size)
     mn = xg.min(axis=4)
     mx = xg.max(axis=4)
-    s, z = _quant_params(mn, mx)
-    codes = _codes(xg, s[..., None], z[..., None]).reshape(B, KVH, N, D)
-    packed = (codes[..., 0::4] | (codes[..., 1::4] << 2) | (codes[..., 2::4] << 4)
-              | (codes[..., 3::4] << 6)).astype(np.uint8)
-    return packed, s.astype(F16), z.astype(F16)
+    s, z = _quant_params(mn, mx, qmax)
+    codes = _codes(xg, s[..., None], z[..., None], qmax).reshape(B, KVH, N, D)
+    return _pack(codes, 3, pf, bits), s.astype(F16), z.astype(F16)
 
 
 def unpack_dequant(packed, scale, zero, full_axis_len, pack_axis, group_size=32, bits=2):
@@ -398,7 +414,7 @@ CACHE_KEYS = (
 )
 
 
-def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=128, sink=4, group_size=32):
+def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=128, sink=4, group_size=32, bits=2):
     """Split a compacted [B, KVH, sink+W, D] cache into the KIVI regimes.
 
     Restates quant_kernel.py:592-622: residual = last ``residual_size`` slots
@@ -427,7 +443,7 @@ def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=128, sink=4
                           ("v_sink", padded(v_compacted), quantize_v),
                           ("k_win", kwin, quantize_k),
                           ("v_win", vwin, quantize_v)):
-        p, s, z = fn(arr, group_size)
+        p, s, z = fn(arr, group_size, bits)
         out[name + "_packed"], out[name + "_scale"], out[name + "_zero"] = p, s, z
     return out
 
@@ -460,7 +476,7 @@ def stream_cache(k_full, v_full, prefill_len, seq_len, window, sink=4, residual_
     return cache, window - residual_size
 
 
-def dequantized_regimes(cache, win_old_len, sink=4, group_size=32):
+def dequantized_regimes(cache, win_old_len, sink=4, group_size=32, bits=2):
     """Dequantized K and V of the whole [sink + W] cache, in slot order.
 
     The composition of test_quantized_attention_correctness.py:40-50: sink
@@ -469,32 +485,32 @@ def dequantized_regimes(cache, win_old_len, sink=4, group_size=32):
     """
     D = cache["k_sink_packed"].shape[-1]
     ks = unpack_dequant(cache["k_sink_packed"], cache["k_sink_scale"], cache["k_sink_zero"],
-                        group_size, 2, group_size)[:, :, :sink]
+                        group_size, 2, group_size, bits)[:, :, :sink]
     vs = unpack_dequant(cache["v_sink_packed"], cache["v_sink_scale"], cache["v_sink_zero"],
-                        D, 3, group_size)[:, :, :sink]
+                        D, 3, group_size, bits)[:, :, :sink]
     parts_k, parts_v = [ks], [vs]
     if win_old_len > 0:
         parts_k.append(unpack_dequant(cache["k_win_packed"], cache["k_win_scale"], cache["k_win_zero"],
-                                      win_old_len, 2, group_size))
+                                      win_old_len, 2, group_size, bits))
         parts_v.append(unpack_dequant(cache["v_win_packed"], cache["v_win_scale"], cache["v_win_zero"],
-                                      D, 3, group_size))
+                                      D, 3, group_size, bits))
     parts_k.append(np.asarray(cache["k_residual"]).astype(F32))
     parts_v.append(np.asarray(cache["v_residual"]).astype(F32))
     return np.concatenate(parts_k, axis=2), np.concatenate(parts_v, axis=2)
 
 
-def quantized_attention(q, win_old_len, cache, sm_scale, sink=4, group_size=32, dtype=np.float64):
+def quantized_attention(q, win_old_len, cache, sm_scale, sink=4, group_size=32, dtype=np.float64, bits=2):
     """Dequantize-then-attend composition of the three regimes.
 
     Restates test_quantized_attention_correctness.py:32-61 (steady state: every
     slot attended).
     """
-    k, v = dequantized_regimes(cache, win_old_len, sink, group_size)
+    k, v = dequantized_regimes(cache, win_old_len, sink, group_size, bits)
     return dense_attention(q, k, v, sm_scale, dtype)
 
 
 def quantized_attention_masked(q, cache, seq_len, window, sm_scale, sink=4, residual_size=128,
-                               group_size=32, dtype=np.float64):
+                               group_size=32, dtype=np.float64, bits=2):
     """What the fused quantized kernel computes, ramp-up included.
 
     The regime composition of quant_kernel.py:358-401 (sink slot s -> sink
@@ -503,13 +519,13 @@ def quantized_attention_masked(q, cache, seq_len, window, sm_scale, sink=4, resi
     kv_indices marks valid (quant_kernel.py:485,496).  Equals
     ``quantized_attention`` in steady state.
     """
-    k, v = dequantized_regimes(cache, max(window - residual_size, 0), sink, group_size)
+    k, v = dequantized_regimes(cache, max(window - residual_size, 0), sink, group_size, bits)
     valid = slot_validity(seq_len, window, sink, 0)
     return masked_attention(q, k, v, valid, sm_scale, dtype)
 
 
 def quantized_attention_varlen(q, cache, seq_lens, window, sm_scale, sink=4, residual_size=128,
-                               group_size=32, dtype=np.float64):
+                               group_size=32, dtype=np.float64, bits=2):
     """quantized_attention_masked per sequence, at that sequence's length
     (the reference's call at one scalar length, quant_kernel.py:551-581,
     applied to each batch row)."""
@@ -518,7 +534,7 @@ def quantized_attention_varlen(q, cache, seq_lens, window, sm_scale, sink=4, res
     for b, n in enumerate(np.asarray(seq_lens).tolist()):
         cb = {key: np.asarray(val)[b:b + 1] for key, val in cache.items()}
         out[b] = quantized_attention_masked(q[b:b + 1], cb, n, window, sm_scale, sink, residual_size,
-                                            group_size, dtype)[0]
+                                            group_size, dtype, bits)[0]
     return out
 
 

@@ -96,7 +96,7 @@ def _dense(**kw):
 def test_dense_validation():
     assert _dense(q=None) == E["NULL"]
     assert _dense(o=None) == E["NULL"]
-    assert _dense(dtype=K.F32) == E["DTYPE"]
+    assert _dense(dtype=7) == E["DTYPE"]           # f16 / f32 / bf16 are taken
     assert _dense(KVH=7) == E["SHAPE"]            # H % KVH != 0
     assert _dense(H=8 * 32, KVH=8) == E["SHAPE"]  # group of 32 > 16 MFMA columns
     assert _dense(D=64) == E["SHAPE"]
@@ -118,7 +118,7 @@ def test_dense_noalloc_validation():
         return K.lib.kvdec_dense_decode_noalloc(a["q"], a["k"], a["v"], a["o"], a["dtype"], a["B"], a["H"],
                                                 a["KVH"], a["L"], a["D"], 0.088, None)
     assert call(q=None) == E["NULL"]
-    assert call(dtype=K.F32) == E["DTYPE"]
+    assert call(dtype=7) == E["DTYPE"]
     assert call(KVH=7) == E["SHAPE"]
     assert call(D=64) == E["SHAPE"]
     assert call(L=0) == E["SEQLEN"]
@@ -176,7 +176,7 @@ def _sparse(**kw):
 
 def test_sparse_validation():
     assert _sparse(v=None) == E["NULL"]
-    assert _sparse(dtype=K.BF16) == E["DTYPE"]
+    assert _sparse(dtype=7) == E["DTYPE"]
     assert _sparse(seq_len=0) == E["SEQLEN"]
     assert _sparse(W=-1) == E["WINDOW"]
     assert _sparse(S=-1) == E["WINDOW"]
@@ -201,8 +201,19 @@ def test_kivi_validation():
     assert _kivi(q=None) == E["NULL"]
     assert _kivi(ptrs=[0x1000] * 5 + [None] + [0x1000] * 6) == E["NULL"]
     assert _kivi(ptrs=[0x1000] * 6 + [None] * 6) == E["NULL"]          # window-old needed at W=256
-    assert _kivi(bits=4) == E["BITS"]
-    assert _kivi(group=64) == E["UNSUPPORTED"]
+    assert _kivi(bits=9) == E["BITS"]
+    assert _kivi(bits=0) == E["BITS"]
+    assert _kivi(group=48) == E["GROUP"]                               # does not divide D_HEAD
+    assert _kivi(bits=1, group=4) == E["GROUP"]                        # not whole bytes of codes
+    # the generic kernel's own checks (widths other than 2, groups other than 32)
+    assert _kivi(bits=4, q=None) == E["NULL"]
+    assert _kivi(bits=4, ptrs=[0x1000] * 6 + [None] * 6) == E["NULL"]
+    assert _kivi(bits=4, S=0) == E["WINDOW"]
+    assert _kivi(group=16, S=17) == E["WINDOW"]                        # sink beyond one group
+    assert _kivi(bits=4, W=128 + 48) == E["GROUP"]
+    assert _kivi(group=64, W=128 + 96) == E["GROUP"]
+    assert _kivi(bits=4, seq_len=0) == E["SEQLEN"]
+    assert _kivi(bits=4, KVH=3) == E["SHAPE"]
     assert _kivi(W=0) == E["WINDOW"]                                  # empty window
     assert _kivi(S=0) == E["WINDOW"]
     assert _kivi(S=33) == E["WINDOW"]
@@ -225,8 +236,10 @@ def _kivi_varlen(**kw):
 def test_kivi_varlen_validation():
     assert _kivi_varlen(lens=None) == E["NULL"]
     assert _kivi_varlen(q=None) == E["NULL"]
-    assert _kivi_varlen(bits=4) == E["BITS"]
-    assert _kivi_varlen(group=64) == E["UNSUPPORTED"]
+    assert _kivi_varlen(bits=9) == E["BITS"]
+    assert _kivi_varlen(group=48) == E["GROUP"]
+    assert _kivi_varlen(bits=4, lens=None) == E["NULL"]
+    assert _kivi_varlen(bits=8, W=200) == E["GROUP"]
     assert _kivi_varlen(W=0) == E["WINDOW"]
     assert _kivi_varlen(W=200) == E["GROUP"]
     assert _kivi_varlen(H=60) == E["SHAPE"]
@@ -245,15 +258,19 @@ def test_quantize_validation(name):
     fn = getattr(K.lib, name)
     assert _quant(fn, x=None) == E["NULL"]
     assert _quant(fn, z=None) == E["NULL"]
-    assert _quant(fn, bits=4) == E["BITS"]
+    assert _quant(fn, bits=9) == E["BITS"]
+    assert _quant(fn, bits=0) == E["BITS"]
     assert _quant(fn, dt=7) == E["DTYPE"]
     assert _quant(fn, N=0) == E["SHAPE"]
-    assert _quant(fn, group=64) == E["UNSUPPORTED"]
     if name == "kvdec_quantize_k":
         assert _quant(fn, N=100) == E["GROUP"]
         assert _quant(fn, D=7) == E["SHAPE"]
+        assert _quant(fn, group=48) == E["GROUP"]                 # 256 tokens not whole groups
+        assert _quant(fn, bits=1, group=4) == E["GROUP"]          # not whole bytes of codes
     else:
         assert _quant(fn, D=100) == E["DGROUP"]
+        assert _quant(fn, group=48) == E["DGROUP"]
+        assert _quant(fn, bits=1, group=4) == E["DGROUP"]
 
 
 def _append(**kw):
@@ -344,7 +361,7 @@ def _svarlen(**kw):
 
 def test_sparse_varlen_validation():
     assert _svarlen(lens=None) == E["NULL"]
-    assert _svarlen(dtype=K.F32) == E["DTYPE"]
+    assert _svarlen(dtype=7) == E["DTYPE"]
     assert _svarlen(W=0, S=0) == E["WINDOW"]
     assert _svarlen(W=-1) == E["WINDOW"]
     assert _svarlen(layout=5) == E["UNSUPPORTED"]

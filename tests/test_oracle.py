@@ -603,3 +603,106 @@ def test_torch_ref_matches_numpy_oracle():
     q16 = q.astype(np.float16)
     np.testing.assert_allclose(T.quantized_attention(t(q16), W - 128, tc, sc).numpy(),
                                O.quantized_attention(q16, W - 128, cache, sc), atol=1e-5)
+
+
+# ----------------------------------------------------------------------------
+# quantizers of any code width (the reference's BITS / GROUP_SIZE parameters)
+# ----------------------------------------------------------------------------
+
+def _exact_codes_q(col, qmax):
+    """Exact-rational clamp(floor(x/s + 1/2) + z, 0, qmax), s = (mx - mn) / qmax."""
+    xs = [Fraction(float(x)) for x in col]
+    mn, mx = min(xs), max(xs)
+    s = (mx - mn) / qmax
+    if s == 0:
+        s = Fraction(1)
+    z = math.floor(-mn / s + Fraction(1, 2))
+    return [min(max(math.floor(x / s + Fraction(1, 2)) + z, 0), qmax) for x in xs], s, z
+
+
+def _field(byte, j, bits):
+    """Code j of a byte, bit by bit (independent of the oracle's shift/mask)."""
+    return sum(((int(byte) >> (j * bits + i)) & 1) << i for i in range(bits))
+
+
+@pytest.mark.parametrize("bits,group", [(1, 16), (3, 16), (4, 32), (4, 64), (8, 16), (2, 64), (5, 8)])
+def test_quantize_any_width_matches_exact_rational_arithmetic(bits, group):
+    qmax, pf = (1 << bits) - 1, 8 // bits
+    r = _rng(40 + bits)
+    N, D = 2 * group, 128
+    x = r.standard_normal((1, 1, N, D)).astype(F32)
+    x[..., 7] *= 10
+    packed, scale, zero = O.quantize_k(x, group, bits)
+    assert packed.shape == (1, 1, N // pf, D) and scale.shape == (1, 1, N // group, D)
+    near = 0
+    for g in range(N // group):
+        for d in range(0, D, 9):
+            col = x[0, 0, group * g:group * (g + 1), d]
+            ec, s, z = _exact_codes_q(col, qmax)
+            assert float(scale[0, 0, g, d]) == float(np.float16(float(s)))
+            assert float(zero[0, 0, g, d]) == float(np.float16(z))
+            for t in range(group):
+                tok = group * g + t
+                got = _field(packed[0, 0, tok // pf, d], tok % pf, bits)
+                if got != ec[t]:
+                    v = Fraction(float(col[t])) / s + Fraction(1, 2)
+                    assert abs(v - round(v)) < Fraction(1, 10**5), "mismatch away from a boundary"
+                    near += 1
+    assert near <= 2
+    v = r.standard_normal((1, 1, 6, D)).astype(F32)
+    packed, scale, zero = O.quantize_v(v, group, bits)
+    assert packed.shape == (1, 1, 6, D // pf) and scale.shape == (1, 1, 6, D // group)
+    for t in range(6):
+        for g in range(D // group):
+            col = v[0, 0, t, group * g:group * (g + 1)]
+            ec, s, z = _exact_codes_q(col, qmax)
+            got = [_field(packed[0, 0, t, (group * g + c) // pf], (group * g + c) % pf, bits) for c in range(group)]
+            assert got == ec
+            assert float(scale[0, 0, t, g]) == float(np.float16(float(s)))
+
+
+def test_quantize_any_width_known_bytes():
+    # bits 1: a group of 8 tokens spanning [0, 1] (s = 1, z = 0): codes = values
+    col = np.array([1, 0, 1, 1, 0, 0, 0, 1], dtype=F32)
+    assert int(O.quantize_k(col[None, None, :, None], 8, 1)[0][0, 0, 0, 0]) == 1 + 4 + 8 + 128
+    # bits 4, two channels per byte: a group of 16 spanning [0, 15]
+    row = np.array([15, 3] + [0] * 14, dtype=F32)
+    assert int(O.quantize_v(row[None, None, None, :], 16, 4)[0][0, 0, 0, 0]) == 15 | 3 << 4
+    # bits 3, two codes per byte at bits 0 and 3: a group of 8 spanning [0, 7]
+    row = np.array([5, 7, 0, 0, 0, 0, 0, 0], dtype=F32)
+    assert int(O.quantize_v(row[None, None, None, :], 8, 3)[0][0, 0, 0, 0]) == 5 | 7 << 3
+    # bits 8: the byte is the code
+    col = np.arange(16, dtype=F32) * 17    # 0 .. 255, s = 1
+    assert O.quantize_k(col[None, None, :, None], 16, 8)[0][0, 0, :, 0].tolist() == (np.arange(16) * 17).tolist()
+    with pytest.raises(ValueError):
+        O.quantize_k(np.zeros((1, 1, 8, 4), F32), 4, 1)     # half a byte of 1-bit codes per group
+
+
+def test_quantized_attention_any_width_is_exact_on_integer_data():
+    """8-bit codes of integer data whose groups span 0..255 dequantize
+    exactly (s = 1, z = 0), so the regime composition must equal dense
+    attention over the original cache: pins the sink padding, window-old and
+    residual slots of the generic width path."""
+    r = _rng(50)
+    B, KVH, G, D, S, W, R, grp = 1, 2, 4, 128, 4, 96, 32, 16
+    n = S + W
+    kc = r.integers(0, 256, (B, KVH, n, D)).astype(F32)
+    vc = r.integers(0, 256, (B, KVH, n, D)).astype(F32)
+    kc[:, :, :S] = kc[:, :, :1]            # the sink group is padded with token 0
+    kc[:, :, 0, :] = 0
+    kc[:, :, 1, :] = 255
+    for g0 in range(S, S + W - R, grp):    # every window-old K group spans 0..255
+        kc[:, :, g0, :] = 0
+        kc[:, :, g0 + 1, :] = 255
+    for c in range(0, D, grp):             # every V channel group spans 0..255
+        vc[:, :, :, c] = 0
+        vc[:, :, :, c + 1] = 255
+    kc16, vc16 = kc.astype(np.float16), vc.astype(np.float16)
+    cache = O.build_quantized_kv_cache(kc16, vc16, residual_size=R, sink=S, group_size=grp, bits=8)
+    q = (r.standard_normal((B, KVH * G, D)) / 64).astype(np.float16)
+    got = O.quantized_attention(q, W - R, cache, SCALE_T, sink=S, group_size=grp, bits=8)
+    want = O.dense_attention(q, kc16, vc16, SCALE_T)
+    assert np.abs(got - want).max() < 1e-9
+
+
+SCALE_T = 128**-0.5
