@@ -1159,6 +1159,7 @@ struct F16LeanArgs {
   int rows;
 };
 
+template <bool TAIL>
 __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
   extern __shared__ __align__(16) char lds[];
   CLOCK_STAMP(A.c, 0);
@@ -1201,10 +1202,36 @@ __global__ __launch_bounds__(kThreads, 1) void f16_lean_kernel(F16LeanArgs A) {
   WaveState st;
   wave_state_init(st);
   if (wave + kWaves < n_tiles) {
+    // 17 tiles (the host's condition: the last one at most 4 rows, rows
+    // 512..515): the last wave also takes the tail, whose rows are its
+    // first loads and its first step (they arrive early, while the two
+    // full tiles stream in); only the tail's rows occupy registers
+    // (a separate instantiation: the tail's registers would cost the
+    // kernel of at most 16 tiles ~0.15 us per step)
+    const bool tail = TAIL && n_tiles > 2 * kWaves && wave == kWaves - 1;
+    u32x4 tk = {0u, 0u, 0u, 0u}, tv[4] = {};
+    if (tail) {
+      const uint32_t t = lane & 15, g = lane >> 4;
+      const TileRows T = rows(2 * kWaves);
+      const uint32_t base = live(2 * kWaves) ? (uint32_t)T.base * kRowBytes + 16u * t : kOOB;
+      // rows past the region read zeros without an access
+      tk = bload16(rk, base + g * kRowBytes);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tv[j] = bload16(rv, base + (4u * g + (uint32_t)j) * kRowBytes);
+    }
     F16Raw X0, X1;
     load_f16(rk, rv, rows(wave), live(wave), 0u, lane, X0);
     load_f16(rk, rv, rows(wave + kWaves), live(wave + kWaves), 0u, lane, X1);
     q_in(true);
+    if (tail) {
+      F16Raw XT;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        XT.k[i] = i == 0 ? tk : u32x4{0u, 0u, 0u, 0u};
+        XT.v[i] = i < 4 ? tv[i] : u32x4{0u, 0u, 0u, 0u};
+      }
+      f16_tile_step(XT, slot, qB, rows(2 * kWaves), A.c.R, A.c.scale_log2, st, lane);
+    }
     f16_tile_step(X0, slot, qB, rows(wave), A.c.R, A.c.scale_log2, st, lane);
     f16_tile_step(X1, slot, qB, rows(wave + kWaves), A.c.R, A.c.scale_log2, st, lane);
   } else if (wave < n_tiles) {
@@ -2132,9 +2159,13 @@ LeanCommon lean_common(const AttnCommon& P) {
 
 // A contiguous fp16 source qualifies when one pass suffices and no wave has
 // more than two tiles.
-bool f16_lean_fits(const AttnCommon& P) {
-  return make_plan(P.pairs, P.n_tiles).splits == 1 && P.n_tiles <= 2 * kWaves &&
-         P.pairs <= 0x7fffffffLL;
+// Up to 16 tiles, or 16 tiles and a tail of at most kLeanTailRows rows
+// (the sink of the W = 512 cache: 516 slots).
+constexpr int kLeanTailRows = 4;
+bool f16_lean_fits(const AttnCommon& P, int64_t rows) {
+  const bool tiles = P.n_tiles <= 2 * kWaves ||
+                     (P.n_tiles == 2 * kWaves + 1 && rows <= 2 * kWaves * kTile + kLeanTailRows);
+  return make_plan(P.pairs, P.n_tiles).splits == 1 && tiles && P.pairs <= 0x7fffffffLL;
 }
 
 int launch_f16_lean(const AttnCommon& P, const _Float16* k, const _Float16* v, int rows,
@@ -2145,7 +2176,12 @@ int launch_f16_lean(const AttnCommon& P, const _Float16* k, const _Float16* v, i
   A.v = v;
   A.rows = rows;
   SET_CLOCK(A.c);
-  hipLaunchKernelGGL(f16_lean_kernel, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes + kQLdsBytes, stream, A);
+  if (P.n_tiles > 2 * kWaves)
+    hipLaunchKernelGGL(f16_lean_kernel<true>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes + kQLdsBytes,
+                       stream, A);
+  else
+    hipLaunchKernelGGL(f16_lean_kernel<false>, dim3((unsigned)P.pairs), dim3(kThreads), kLdsBytes + kQLdsBytes,
+                       stream, A);
   return launch_status();
 }
 
@@ -2641,7 +2677,7 @@ int kvdec_dense_decode(const void* q, const void* k, const void* v, void* o, int
   P.n_tiles = (int)tiles_for(KVDEC_KIND_DENSE, L);
   P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
   P.R = SlotRanges{(int)L, 0, 0};
-  if (f16_lean_fits(P))
+  if (f16_lean_fits(P, L))
     return launch_f16_lean(P, static_cast<const _Float16*>(k), static_cast<const _Float16*>(v), (int)L,
                            static_cast<hipStream_t>(stream));
   F16Src S{static_cast<const _Float16*>(k), static_cast<const _Float16*>(v), (int)L};
@@ -2723,7 +2759,7 @@ int kvdec_sparse_decode(const void* q, const void* k_cache, const void* v_cache,
   P.n_tiles = (int)tiles_for(KVDEC_KIND_SPARSE, n);
   P.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
   P.R = sparse_ranges(seq_len, window, sink, layout);
-  if (f16_lean_fits(P))
+  if (f16_lean_fits(P, n))
     return launch_f16_lean(P, static_cast<const _Float16*>(k_cache), static_cast<const _Float16*>(v_cache),
                            (int)n, static_cast<hipStream_t>(stream));
   F16Src S{static_cast<const _Float16*>(k_cache), static_cast<const _Float16*>(v_cache), (int)n};

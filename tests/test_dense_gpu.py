@@ -28,7 +28,7 @@ def test_dense_golden(device):
     assert max_abs(o, g["o"]) < ATTN_TOL
 
 
-@pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 100, 1000, 4097, 8192])
+@pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 100, 1000, 4097, 8192, 513, 516, 512])
 def test_dense_lengths(L, device):
     B, H, KVH, D = 4, 64, 8, 128
     q = randn((B, H, D), L)

@@ -119,3 +119,24 @@ def test_sparse_rejects_bad_cache_shape(device):
         sparse_decode_attention(q, kc, kc, seq_len=1000, window=256)
     with pytest.raises(ValueError):
         sparse_decode_attention(q, kc, kc, seq_len=1000, window=255, layout="spiral")
+
+
+@pytest.mark.parametrize("W", [508, 512])
+def test_sparse_sixteen_tiles_and_a_tail(W, device):
+    """W=508 fills the lean kernel's 16 tiles exactly; W=512 (516 slots)
+    adds a tail of 4 rows that the lean kernel's last wave steps first.
+    Steady state (both layouts), ramp-up through the tail, and 1e4 garbage
+    in slots not yet written."""
+    B, H, KVH, D = 4, 64, 8, 128
+    q = randn((B, H, D), W).astype(np.float16)
+    kc = randn((B, KVH, S + W, D), W + 1).astype(np.float16)
+    vc = randn((B, KVH, S + W, D), W + 2).astype(np.float16)
+    for L, layout in ((163840, "linear"), (163840, "ring"), (S + W - 2, "linear"), (S + W - 2, "ring"),
+                      (300, "linear")):
+        say(f"sparse W={W} L={L} {layout}")
+        valid = O.slot_validity(L, W, S, 0 if layout == "linear" else 1)
+        k = np.where(valid[None, None, :, None], kc, np.float16(1e4))
+        v = np.where(valid[None, None, :, None], vc, np.float16(1e4))
+        o = _run(q, k, v, L, W, device, layout=layout)
+        ref = O.masked_attention(q, kc, vc, valid, SCALE)
+        assert max_abs(o, ref) < ATTN_TOL, (L, layout)
