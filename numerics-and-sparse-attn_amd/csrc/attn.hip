@@ -263,17 +263,68 @@ __device__ __forceinline__ void publish_f(const AttnCommon& P, const WaveState& 
   }
 }
 
+// Packed layout, remainder rows folded on the way out with VALU lane swaps:
+// for rows r = 2p, 2p + 1 of an accumulator, v_permlane32_swap leaves
+// (row 2p of lanes 0..31, row 2p + 1 of lanes 0..31) in one register and
+// the same rows of lanes 32..63 in the other, so their sum holds, in lane
+// L < 32, head 4g + 2p plus its remainder (lane L + 32) and, in lane
+// L + 32, head 4g + 2p + 1 plus its remainder, g = L >> 4.  Each lane
+// then writes its head's adjacent channel pair of every (grp, p): 8
+// eight-byte writes of heads 0..7 (rows 8..15 are not written; the merges
+// read heads only).  ADD as in publish_q.  The elements are copied to
+// scalars before their bit casts: ROCm 7.2 clang compiles
+// `__builtin_bit_cast` of a vector element (`v[i]`) as a read of element 0.
+template <bool ADD>
+__device__ __forceinline__ void publish_q_folded(const QState& qs, char* slot, int lane) {
+  const int t = lane & 15, g = lane >> 4;
+  const int hb = g < 2 ? 4 * g : 4 * (g - 2) + 1;
+  float2v v[4][2];
+  uint32_t off[4][2];
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int ch = q_state_channel(grp, 0, t);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      off[grp][p] = row_off(hb + 2 * p, ch >> 2) + 4 * (ch & 3);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const float fx = qs.O[2 * grp + c][2 * p], fy = qs.O[2 * grp + c][2 * p + 1];
+        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, fx),
+                                                         __builtin_bit_cast(uint32_t, fy), false, false);
+        v[grp][p][c] = __builtin_bit_cast(float, (uint32_t)sw[0]) + __builtin_bit_cast(float, (uint32_t)sw[1]);
+      }
+    }
+  }
+  if (ADD) {
+    float2v prev[4][2];
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) prev[grp][p] = *reinterpret_cast<const float2v*>(slot + off[grp][p]);
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) v[grp][p] += prev[grp][p];
+  }
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) *reinterpret_cast<float2v*>(slot + off[grp][p]) = v[grp][p];
+}
+
 // Quantized-tile accumulators: lane (t, g) holds head 4g + r of channels
 // q_state_channel(grp, 0..1, t) (adjacent) in QState::O[2 grp + 0..1]; each
-// pair goes out as one 8-byte write.  All 16 head rows are written (rows of heads >= G stay inside the
-// wave's slot and the merge never reads them), so no write is predicated.
-// ADD: the slot already holds this wave's fp16-tile rows (all reads are
-// issued before any write, so the adds wait on LDS once).  PACK: the
-// remainder rows are folded in first (rows 8..15 then repeat heads 0..7),
-// or, with FOLD false, published as rows 8..15 for the merge to add.
-template <bool ADD, bool PACK = false, bool FOLD = true>
-__device__ __forceinline__ void publish_q(QState& qs, char* slot, int lane) {
-  if (PACK && FOLD) q_state_fold(qs);
+// pair goes out as one 8-byte write.  All 16 head rows are written (rows of
+// heads >= G stay inside the wave's slot and the merge never reads them), so
+// no write is predicated.  ADD: the slot already holds this wave's fp16-tile
+// rows (all reads are issued before any write, so the adds wait on LDS
+// once).  PACK: publish_q_folded.
+template <bool ADD, bool PACK = false>
+__device__ __forceinline__ void publish_q(const QState& qs, char* slot, int lane) {
+  if (PACK) {
+    publish_q_folded<ADD>(qs, slot, lane);
+    return;
+  }
   const int t = lane & 15, g = lane >> 4;
   float2v v[4][4];
   uint32_t off[4][4];
@@ -1010,10 +1061,6 @@ __device__ __forceinline__ void q_operand_read(const char* qarea, int lane, half
   }
 }
 
-// Barrier, then one thread per (head, 4 channels) combines the 8 waves'
-// published partials into the fp16 output rows of this KV head.  Waves
-// below NPACK published packed quantized rows unfolded: their row hn + 8
-// (the remainder part) is added to row hn.
 // LDS of a lean kernel with NW waves: the maxima and sums of every wave's
 // partial (16 heads each), then one 8 KB slot per wave; the Q area follows.
 // NW = 8 is attn_kernel's layout (kLdsM, kLdsL, kLdsSlots, kLdsBytes).
@@ -1030,10 +1077,9 @@ static_assert(LeanLds<kWaves>::kL == kLdsL && LeanLds<kWaves>::kSlots == kLdsSlo
 
 // Barrier, then one thread per (head, 4 channels) combines the NW waves'
 // published partials into the fp16 output rows of this KV head.  The waves
-// of bit mask PMASK published packed quantized rows unfolded: their row
-// hn + 8 (the remainder part) is added to row hn.  The waves of bit mask
-// SKIP (never wave 0) have had their partials combined into another's.
-template <unsigned PMASK = 0, int NW = kWaves, unsigned SKIP = 0>
+// of bit mask SKIP (never wave 0) have had their partials combined into
+// another's.
+template <int NW = kWaves, unsigned SKIP = 0>
 __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds, uint32_t head) {
   typedef LeanLds<NW> Lds;
   static_assert((SKIP & 1u) == 0, "wave 0's partial is always read");
@@ -1052,14 +1098,6 @@ __device__ __forceinline__ void lean_merge(const LeanCommon& C, const char* lds,
     lw[w] = sh_l[w * kMaxGroup + hn];
     ow[w] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn, ch));
   }
-  float4v orem[NW];
-#pragma unroll
-  for (int w = 0; w < NW; ++w)
-    if ((PMASK >> w) & 1u)
-      orem[w] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn + 8, ch));
-#pragma unroll
-  for (int w = 0; w < NW; ++w)
-    if ((PMASK >> w) & 1u) ow[w] += orem[w];
   float M = mw[0];
 #pragma unroll
   for (int w = 1; w < NW; ++w)
@@ -1103,10 +1141,9 @@ __device__ __forceinline__ void lean_publish_f(int G, const WaveState& st, char*
 // in (`count`, zeroed before the workgroup's first barrier), waits for the
 // four (a bounded poll; should it run out, the output is NaN), then wave w
 // combines heads 2w, 2w + 1 (and 2w + 8, 2w + 9 when G > 8): one thread
-// per (head, 4 channels), packed remainder rows (PACK) folded in.  The
-// threads of a head sit in one wave, whose reads of the four partials are
-// issued before its writes into wave 0's.
-template <bool PACK, int NW>
+// per (head, 4 channels).  The threads of a head sit in one wave, whose
+// reads of the four partials are issued before its writes into wave 0's.
+template <int NW>
 __device__ __forceinline__ void quad_premerge(int G, char* lds, int* count, int lane, int wave) {
   typedef LeanLds<NW> Lds;
   if (lane == 0) __hip_atomic_fetch_add(count, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1129,8 +1166,6 @@ __device__ __forceinline__ void quad_premerge(int G, char* lds, int* count, int 
       mw[w] = sh_m[w * kMaxGroup + hn];
       lw[w] = sh_l[w * kMaxGroup + hn];
       ow[w] = *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn, ch));
-      if (PACK)
-        ow[w] += *reinterpret_cast<const float4v*>(lds + Lds::kSlots + w * kSlotBytes + row_off(hn + 8, ch));
     }
     float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
     float L = 0.f;
@@ -1329,7 +1364,7 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     if (i0 < n_q) step(i0, X0);
     if (i1 < n_q) step(i1, X1);
     lean_publish_ml(A.c.G, st, lds, lane, wave);
-    publish_q<false, PACK, false>(qs, slot, lane);
+    publish_q<false, PACK>(qs, slot, lane);
   } else {
     // residual tile w - 4: rows 32 (w - 4) .. + 31 (interleaving the four
     // tiles' rows, or issuing V after the softmax, measured slower here:
@@ -1351,7 +1386,7 @@ __global__ __launch_bounds__(kThreads, 1) void kivi_lean_kernel(KiviLeanArgs A) 
     lean_publish_ml(A.c.G, st, lds, lane, wave);
     lean_publish_f(A.c.G, st, slot, lane);
   }
-  lean_merge<PACK ? 0xFu : 0u>(A.c, lds, head);   // PACK: waves 0..3 left their rows unfolded
+  lean_merge(A.c, lds, head);
 }
 
 // The lean KIVI kernel for exactly 4 window-old groups (W = 256 with
@@ -1410,8 +1445,8 @@ __global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLea
       q_tile_step<false, PACK>(X, slot, qB, sk ? 0 : A.sink + kTile * wave, sk ? A.sink : kTile, A.c.R,
                                sl2, st, qs, lane);
     lean_publish_ml<kLean9Waves>(A.c.G, st, lds, lane, wave);
-    publish_q<false, PACK, false>(qs, slot, lane);
-    if (wave < 4) quad_premerge<PACK, kLean9Waves>(A.c.G, lds, premerge_count, lane, wave);
+    publish_q<false, PACK>(qs, slot, lane);
+    if (wave < 4) quad_premerge<kLean9Waves>(A.c.G, lds, premerge_count, lane, wave);
   } else {
     // residual tile w - 5, its loads after the barrier (as in kivi_lean_kernel)
     const int tile = wave - 5;
@@ -1433,7 +1468,7 @@ __global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLea
     lean_publish_f(A.c.G, st, slot, lane);
   }
   // waves 0..3 are in wave 0's partial; PACK: wave 4 left its rows unfolded
-  lean_merge<PACK ? 0x10u : 0u, kLean9Waves, 0xEu>(A.c, lds, head);
+  lean_merge<kLean9Waves, 0xEu>(A.c, lds, head);
 }
 
 // The decode-time KIVI cache's decode over rings of 5 tiles (residual 128)
@@ -1687,8 +1722,8 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
       }
     }
     lean_publish_ml<kStepWaves>(A.c.G, st, lds, lane, wave);
-    publish_q<false, PACK, false>(qs, slot, lane);
-    if (wave < 4) quad_premerge<PACK, kStepWaves>(A.c.G, lds, premerge_count, lane, wave);
+    publish_q<false, PACK>(qs, slot, lane);
+    if (wave < 4) quad_premerge<kStepWaves>(A.c.G, lds, premerge_count, lane, wave);
     if (MODE == kRingStep && sk && lane == 0) {
       // the workgroup's arrival, once the sink wave has published: a wait
       // for the atomic's return waits for every memory operation the wave
@@ -1758,7 +1793,7 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
     }
   }
   // waves 0..3 are in wave 0's partial; PACK: wave 4 left its rows unfolded
-  lean_merge<PACK ? 0x10u : 0u, kStepWaves, 0xEu>(A.c, lds, pair);
+  lean_merge<kStepWaves, 0xEu>(A.c, lds, pair);
   // the step's record, by the last of the sequence's workgroups to arrive
   // (after the merge: the arrival atomic's round trip does not hold the
   // merge's barrier back)
@@ -1883,10 +1918,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs
     q_tile_body<false, true, PACK>(slot, qB, 0, A.sink, A.c.R, sl2, slack, st, qs, lane);
   }
   wide_publish_ml(A.c.G, st, lds, lane, wave);
-  publish_q<false, PACK, false>(qs, slot, lane);
+  publish_q<false, PACK>(qs, slot, lane);
 
   // merge: one thread per (head, 4 channels) over the 16 quantized partials
-  // (rows hn + 8 hold the packed remainder parts) and the 4 fp16 partials
+  // (remainders already folded in) and the 4 fp16 partials
   __syncthreads();
   const int e = threadIdx.x;
   if (e >= A.c.G * 32) return;
@@ -1905,7 +1940,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs
 #pragma unroll
   for (int p0 = 0; p0 < kWideParts; p0 += 4) {
     float lw[4];
-    float4v ow[4], orem[4];
+    float4v ow[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int p = p0 + j;
@@ -1913,14 +1948,13 @@ __global__ __launch_bounds__(kWideThreads, 1) void kivi_wide_kernel(KiviLeanArgs
       const char* part = p < kWideWaves ? lds + kWideLdsSlots + p * kSlotBytes
                                         : lds + kWideLdsF16 + (p - kWideWaves) * kWideF16Bytes;
       ow[j] = *reinterpret_cast<const float4v*>(part + row_off(hn, ch));
-      if (PACK && p < kWideWaves) orem[j] = *reinterpret_cast<const float4v*>(part + row_off(hn + 8, ch));
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int p = p0 + j;
       const float f = __builtin_amdgcn_exp2f(mw[p] - M);
       L += lw[j] * f;
-      acc += (PACK && p < kWideWaves ? ow[j] + orem[j] : ow[j]) * f;
+      acc += ow[j] * f;
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;

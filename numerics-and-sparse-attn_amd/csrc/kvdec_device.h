@@ -620,22 +620,6 @@ __device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lan
   for (int b = 0; b < 8; ++b) qs.O[b] = qs.O[b] * ar;
 }
 
-// Packed layout: rows 8..15 of each accumulator hold the remainder parts of
-// heads 0..7; add them to rows 0..7 (lanes L and L ^ 32), leaving the sums in
-// both halves.  The exchange goes through ds_bpermute: this toolchain (ROCm
-// 7.2 clang) miscompiles v_permlane32_swap applied to the elements of a
-// vector (the elements after the first are replaced by the first's result).
-__device__ __forceinline__ void q_state_fold(QState& qs) {
-#pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    const float4v x = qs.O[b];
-    float4v y;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) y[r] = __shfl_xor(x[r], 32);
-    qs.O[b] = x + y;
-  }
-}
-
 // Layout of a staged KIVI tile inside a wave slot (bytes):
 //   [0, 1024)     K codes, 8 byte rows x 128 channels (as stored)
 //   [1024, 1280)  K scales [128], [1280, 1536) negated K zeros [128]
@@ -797,7 +781,7 @@ constexpr float kSlackVScale = 128.0f;
 // 8..15, so one MFMA per block covers both and lanes n, n + 8 add their
 // logits (zero term included); PV's A operand holds P' rounded to fp16 in
 // rows 0..7 and the remainder in rows 8..15, which the accumulators keep
-// apart until q_state_fold.  The remainder is fp16(pr * scale + e), where
+// apart until they are published.  The remainder is fp16(pr * scale + e), where
 // pB + pr is p (pr = fp16(p - pB)) and e = pB * scale - fp16(pB * scale) is
 // exact: ~2^-21 of P' instead of ~2^-22.  Lanes of both halves take each
 // operand from one instruction sequence: the lane mask zeroes the
