@@ -621,19 +621,23 @@ __device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lan
 }
 
 // Layout of a staged KIVI tile inside a wave slot (bytes):
-//   [0, 1024)     K codes, 8 byte rows x 128 channels (as stored)
-//   [1024, 1280)  K scales [128], [1280, 1536) negated K zeros [128]
-//   [1536, 2560)  V codes, 32 token rows x 32 bytes (as stored; read back
+//   [0, 1280)     K codes, 8 byte rows x 128 channels (as stored), rows
+//                 kQsKRow = 160 bytes apart: QK reads rows 4 blk + 0..3 at
+//                 once, which 128-byte rows would put in the same LDS banks
+//   [1280, 1536)  K scales [128], [1536, 1792) negated K zeros [128]
+//   [1792, 2816)  V codes, 32 token rows x 32 bytes (as stored; read back
 //                 transposed by ds_read_b64_tr_b8)
-//   [2560, 2816)  V scales transposed [4 groups][32 tokens],
-//   [2816, 3072)  negated V zeros transposed
-constexpr int kQsK = 0, kQsKS = 1024, kQsKZ = 1280, kQsV = 1536, kQsVS = 2560, kQsVZ = 2816;
-constexpr int kQsBytes = 3072;
+//   [2816, 3072)  V scales transposed [4 groups][32 tokens],
+//   [3072, 3328)  negated V zeros transposed
+constexpr int kQsKRow = 160;
+constexpr int kQsK = 0, kQsKS = 1280, kQsKZ = 1536, kQsV = 1792, kQsVS = 2816, kQsVZ = 3072;
+constexpr int kQsBytes = 3328;
+static_assert(kQsBytes <= kSlotBytes, "a staged KIVI tile fits a wave slot");
 constexpr uint32_t kNegPk = 0x80008000u;   // sign bits of an fp16 pair
 constexpr uint32_t kOnePk = 0x3C003C00u;   // fp16 pair (1, 1)
 
 __device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
-  *reinterpret_cast<u32x4*>(slot + kQsK + 16 * lane) = X.kc;
+  *reinterpret_cast<u32x4*>(slot + kQsK + kQsKRow * (lane >> 3) + 16 * (lane & 7)) = X.kc;
   *reinterpret_cast<uint32_t*>(slot + kQsKS + 4 * lane) = X.ks;
   *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = X.kz ^ kNegPk;
   *reinterpret_cast<u32x4*>(slot + kQsV + 16 * lane) = X.vc;
@@ -823,7 +827,7 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
 #pragma unroll
     for (int blk = 0; blk < (HALF ? 1 : 2); ++blk) {
       const u32x2 w =
-          *reinterpret_cast<const u32x2*>(slot + kQsK + (4 * blk + (t >> 2)) * 128 + 32 * c + 8 * g);
+          *reinterpret_cast<const u32x2*>(slot + kQsK + (4 * blk + (t >> 2)) * kQsKRow + 32 * c + 8 * g);
       const u32x2 f = fields2(w, sh);
       const u32x2 d0 = codes_f16(f[0], kCodeScale), d1 = codes_f16(f[1], kCodeScale);
       const u32x4 d = {d0[0], d0[1], d1[0], d1[1]};
