@@ -378,14 +378,17 @@ def test_quantized_attention_rejects_small_window(device):
         _attend(q, cache, 1000, 64)
 
 
-@pytest.mark.parametrize("sink", [1, 16, 17, 32])
+@pytest.mark.parametrize("sink", [1, 16, 17, 20, 32])
 @pytest.mark.parametrize("W", [256, 1024])
 def test_quantized_attention_sink_sizes(sink, W, device):
     """Sink groups of 1 to 32 real tokens (the API's sink argument): the
-    9-wave lean kernel (W=256, the sink group on wave 8: a half-group step
+    9-wave lean kernel (W=256, the sink group on wave 4: a half-group step
     up to 16 tokens, a whole one above), the 16-wave kernel (W=1024 with a sink of at
     most 16 tokens: its half-group step after the loop) and the work-queue
-    kernel (W=1024, sink > 16), in steady state and ramp-up."""
+    kernel (W=1024, sink > 16), in steady state and ramp-up.  Each case is
+    launched five times and every output checked: a schedule whose result
+    depends on how the waves interleave shows as a wrong output on some
+    calls only."""
     from quant_kernel import build_quantized_kv_cache
     B, H, KVH, D = 2, 16, 2, 128
     q16 = randn((B, H, D), 60 + sink + W, np.float16)
@@ -396,11 +399,13 @@ def test_quantized_attention_sink_sizes(sink, W, device):
         say(f"kivi sink={sink} W={W} L={L}")
         cache = build_quantized_kv_cache(dev(kc.astype(np.float16), device), dev(vc.astype(np.float16), device),
                                          sink=sink)
-        o = _attend(dev(q16, device), cache, L, W, sink=sink)
         ref = O.quantized_attention_masked(q16, _host_cache(cache), L, W, SCALE, sink=sink)
-        assert max_abs(o, ref) < ATTN_TOL
-        if L > sink + W:
-            assert_nearly_rounded(o, ref)
+        qd = dev(q16, device)
+        for rep in range(5):
+            o = _attend(qd, cache, L, W, sink=sink)
+            assert max_abs(o, ref) < ATTN_TOL, rep
+            if L > sink + W:
+                assert_nearly_rounded(o, ref)
 
 
 @pytest.mark.parametrize("W", [256, 1024])
