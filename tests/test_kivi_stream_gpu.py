@@ -127,3 +127,39 @@ def test_stream_rejects_short_prefill(device):
     k = torch.zeros(1, 2, S + 255, 128, dtype=torch.float16, device=device)
     with pytest.raises(ValueError):
         KiviStreamCache.from_prefill(k, k, 256)
+
+
+@pytest.mark.parametrize("per_sequence", [False, True])
+def test_stream_attend_bit_identical_under_concurrent_load(per_sequence, device):
+    """The ring decode kernel's waves (window-old slots, the sink group, the
+    ring tiles) meet only at the Q readiness count, the premerge count and
+    the merge barrier, and its work split is static: repeated attends of one
+    state, some launched while a second stream copies 512 MiB through the
+    same CUs and HBM, must be bit-identical to the first (one ring state for
+    all sequences, and one per sequence)."""
+    from kivi_stream import KiviStreamBatch, KiviStreamCache
+    B, H, KVH, W, D = 32, 64, 8, 256, 128
+    L0 = S + W + 40
+    gen = torch.Generator(device="cuda").manual_seed(97)
+    kf = torch.randn(B, KVH, L0, D, generator=gen, device="cuda", dtype=torch.float16)
+    vf = torch.randn(B, KVH, L0, D, generator=gen, device="cuda", dtype=torch.float16)
+    q = torch.randn(B, H, D, generator=gen, device="cuda", dtype=torch.float16)
+    cls = KiviStreamBatch if per_sequence else KiviStreamCache
+    cache = cls.from_prefill(kf, vf, W)
+    say(f"stream concurrent-load determinism per_sequence={per_sequence}")
+    ref = cache.attend(q)
+    torch.cuda.synchronize()
+    src = torch.ones((512 << 20) // 4, dtype=torch.int32, device=device)
+    dst = torch.empty_like(src)
+    side = torch.cuda.Stream(device)
+    outs = []
+    for i in range(16):
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            dst.copy_(src)
+        if i % 2:
+            torch.cuda.current_stream(device).wait_stream(side)
+        outs.append(cache.attend(q))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert torch.equal(o, ref), f"attend {i} differs from the first"

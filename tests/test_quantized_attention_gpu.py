@@ -408,8 +408,8 @@ def test_quantized_attention_sink_sizes(sink, W, device):
                 assert_nearly_rounded(o, ref)
 
 
-@pytest.mark.parametrize("W", [256, 1024])
-def test_kivi_bit_identical_under_concurrent_load(W, device):
+@pytest.mark.parametrize("W,sink", [(32, 4), (160, 4), (256, 4), (256, 20), (352, 4), (1024, 4), (1024, 20)])
+def test_kivi_bit_identical_under_concurrent_load(W, sink, device):
     """The fused decode's waves meet only at the Q readiness count (lean
     kernels), the group-queue counter (16-wave kernel) and the merge barrier,
     so a result must not depend on how far each wave has got.  Launches made
@@ -417,21 +417,23 @@ def test_kivi_bit_identical_under_concurrent_load(W, device):
     CUs and HBM must be bit-identical to a launch on an idle GPU (the lean
     kernel's work split is static; the 16-wave kernel's queue makes the
     summation order vary, so there the outputs must agree within the
-    attention gate and the oracle's)."""
+    attention gate and the oracle's).  The windows cover the 8-wave lean
+    kernel (W=32, 160, 352), the 9-wave one (W=256, with a half- and a
+    whole-group sink step) and the 16-wave one (W=1024, sink of 4 and 20)."""
     from quant_kernel import build_quantized_kv_cache, sparse_decode_attention_quantized
     B, H, KVH, D = 32, 64, 8, 128
-    L = S + W + 1000
-    gen = torch.Generator(device=device).manual_seed(70 + W)
-    kc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
-    vc = torch.randn(B, KVH, S + W, D, generator=gen, device=device, dtype=torch.float16)
+    L = sink + W + 1000
+    gen = torch.Generator(device=device).manual_seed(70 + W + sink)
+    kc = torch.randn(B, KVH, sink + W, D, generator=gen, device=device, dtype=torch.float16)
+    vc = torch.randn(B, KVH, sink + W, D, generator=gen, device=device, dtype=torch.float16)
     q = torch.randn(B, H, D, generator=gen, device=device, dtype=torch.float16)
-    cache = build_quantized_kv_cache(kc, vc)
+    cache = build_quantized_kv_cache(kc, vc, sink=sink)
     args = [cache[k] for k in O.CACHE_KEYS]
 
     def attend():
-        return sparse_decode_attention_quantized(q, *args, seq_len=L, window=W)
+        return sparse_decode_attention_quantized(q, *args, seq_len=L, window=W, sink=sink)
 
-    say(f"kivi concurrent-load determinism W={W}")
+    say(f"kivi concurrent-load determinism W={W} sink={sink}")
     ref = attend()
     torch.cuda.synchronize()
     src = torch.ones((512 << 20) // 4, dtype=torch.int32, device=device)
@@ -455,5 +457,5 @@ def test_kivi_bit_identical_under_concurrent_load(W, device):
         else:
             assert max_abs(host(o), o_ref) < 1e-3, f"launch {i}"
     hc = _host_cache(cache)
-    ho = O.quantized_attention(host(q)[:2], W - R, {k: v[:2] for k, v in hc.items()}, SCALE)
+    ho = O.quantized_attention_masked(host(q)[:2], {k: v[:2] for k, v in hc.items()}, L, W, SCALE, sink=sink)
     assert max_abs(o_ref[:2], ho) < ATTN_TOL
