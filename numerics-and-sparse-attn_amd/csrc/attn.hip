@@ -1467,7 +1467,7 @@ __global__ __launch_bounds__(64 * kLean9Waves, 1) void kivi_lean9_kernel(KiviLea
     lean_publish_ml<kLean9Waves>(A.c.G, st, lds, lane, wave);
     lean_publish_f(A.c.G, st, slot, lane);
   }
-  // waves 0..3 are in wave 0's partial; PACK: wave 4 left its rows unfolded
+  // waves 0..3 are in wave 0's partial
   lean_merge<kLean9Waves, 0xEu>(A.c, lds, head);
 }
 
@@ -1792,7 +1792,7 @@ __global__ __launch_bounds__(64 * kStepWaves, 1) void kivi_ring_kernel(StepLeanA
       *reinterpret_cast<u32x4*>(dst) = g == 0 ? kn : vn;
     }
   }
-  // waves 0..3 are in wave 0's partial; PACK: wave 4 left its rows unfolded
+  // waves 0..3 are in wave 0's partial
   lean_merge<kStepWaves, 0xEu>(A.c, lds, pair);
   // the step's record, by the last of the sequence's workgroups to arrive
   // (after the merge: the arrival atomic's round trip does not hold the
