@@ -152,3 +152,96 @@ def test_random_shapes_against_oracle(seed, device):
         assert np.array_equal(np.isnan(o), nan), f"case {case}: {desc}: NaN elements differ from the oracle's"
         err = float(np.abs(o[~nan] - ref[~nan]).max()) if (~nan).any() else 0.0
         assert err < TOL.get(kind, ATTN_TOL), f"case {case}: {desc}: max error {err:.3e}"
+
+
+def _values(rng, shape, dtype):
+    """Inputs of a random character: plain normals, a huge or tiny overall
+    scale, constant stretches (zero-range groups) and single outliers."""
+    x = rng.standard_normal(shape).astype(np.float32)
+    mode = int(rng.integers(5))
+    if mode == 1:
+        x *= np.float32(2.0 ** int(rng.integers(-20, 12)))
+    elif mode == 2:
+        x[..., ::3] = np.float32(rng.standard_normal())
+    elif mode == 3:
+        x.reshape(-1)[rng.integers(x.size, size=8)] *= 1000
+    elif mode == 4:
+        x = np.round(x * 4) / 4                      # many exact ties with the code grid
+    t = torch.from_numpy(x).to(dtype)
+    if dtype == torch.float16:
+        t = torch.nan_to_num(t, posinf=65504.0, neginf=-65504.0)
+    return t
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_random_quantizer_inputs_bit_exact(seed, device):
+    """quantize_k_cache / quantize_v_cache on random shapes, input dtypes and
+    value patterns (wide and tiny ranges, constant groups, outliers, values
+    on the code grid): codes, scales and zeros bit-identical to the oracle's
+    (IEEE float32 with correctly rounded division)."""
+    from quant_kernel import quantize_k_cache, quantize_v_cache
+    rng = np.random.default_rng(2000 + seed)
+    for case in range(40):
+        dtype = [torch.float16, torch.bfloat16, torch.float32][int(rng.integers(3))]
+        B, KVH = int(rng.integers(1, 4)), int(rng.integers(1, 9))
+        N = 32 * int(rng.integers(1, 12))
+        x = _values(rng, (B, KVH, N, 128), dtype)
+        xh = x.float().numpy()
+        for fn, ofn in ((quantize_k_cache, O.quantize_k), (quantize_v_cache, O.quantize_v)):
+            say(f"random quantizer case {case}: {fn.__name__} {dtype} B={B} KVH={KVH} N={N}")
+            got = [host(t) for t in fn(x.to(device))]
+            torch.cuda.synchronize()
+            for name, g, w in zip(("packed", "scale", "zero"), got, ofn(xh)):
+                np.testing.assert_array_equal(g, w, err_msg=f"case {case} {fn.__name__} {name}")
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_random_stream_sequences(seed, device):
+    """The decode-time cache driven by a random mix of append, reserve (row
+    written afterwards) and step_attend calls from a random prefill, attended
+    at random points: the output matches the oracle's stream_cache state at
+    that length (one ring state for all sequences, and one per sequence)."""
+    from kivi_stream import KiviStreamBatch, KiviStreamCache
+    rng = np.random.default_rng(3000 + seed)
+    for case in range(6):
+        H, KVH = GROUPINGS[int(rng.integers(len(GROUPINGS)))]
+        B, D = int(rng.integers(1, 4)), 128
+        W = int(rng.choice([128, 160, 224, 256, 288, 352, 384, 512]))
+        L0 = 4 + W + int(rng.integers(0, 100))
+        steps = int(rng.integers(20, 90))
+        kf = _rn(rng, (B, KVH, L0 + steps, D))
+        vf = _rn(rng, (B, KVH, L0 + steps, D))
+        q = _rn(rng, (B, H, D))
+        per_seq = bool(rng.random() < 0.5)
+        cls = KiviStreamBatch if per_seq else KiviStreamCache
+        kd, vd, qd = dev(kf, device), dev(vf, device), dev(q, device)
+        cache = cls.from_prefill(kd[:, :, :L0], vd[:, :, :L0], W)
+        L = L0
+        for step in range(steps):
+            op = int(rng.integers(3))
+            if op == 0 or (op == 2 and not per_seq):
+                cache.append(kd[:, :, L], vd[:, :, L])
+                o = None
+            elif op == 1:
+                if per_seq:   # the ring row each sequence takes
+                    rows = cache.reserve().cpu().tolist()
+                    for b, r in enumerate(rows):
+                        cache.t["k_ring"][b, :, r] = kd[b, :, L]
+                        cache.t["v_ring"][b, :, r] = vd[b, :, L]
+                else:
+                    kv, vv = cache.reserve()
+                    kv.copy_(kd[:, :, L])
+                    vv.copy_(vd[:, :, L])
+                o = None
+            else:
+                o = cache.step_attend(qd, kd[:, :, L], vd[:, :, L])
+            L += 1
+            if o is None and rng.random() < 0.2:
+                o = cache.attend(qd)
+            if o is not None:
+                say(f"random stream case {case}: per_seq={per_seq} B={B} H={H} KVH={KVH} W={W} L0={L0} L={L}")
+                torch.cuda.synchronize()
+                sc, wlen = O.stream_cache(kf, vf, L0, L, W)
+                ref = O.quantized_attention(q, wlen, sc, SCALE)
+                err = float(np.abs(host(o).astype(np.float64) - ref).max())
+                assert err < ATTN_TOL, f"case {case} L={L}: max error {err:.3e}"
