@@ -234,6 +234,28 @@ int kvdec_sparse_decode_kivi_varlen(const void* q, const void* k_res, const void
                                     float sm_scale, void* stream);
 
 /*
+ * kvdec_sparse_decode_kivi / _varlen with the element types of the query
+ * and of the residual rows as arguments: quant_kernel.py:436-548 loads q and
+ * the fp16 residual cache (K_cache_ptr, V_cache_ptr) in whatever dtype they
+ * come in, computes in fp32 and stores o in q's dtype (:548), and
+ * build_quantized_kv_cache keeps the residual in the compacted cache's dtype
+ * (quant_kernel.py:592-593).
+ *   q, o   : [B, H, D] of q_dtype (KVDEC_F16, KVDEC_BF16 or KVDEC_F32)
+ *   k_res, v_res : residual rows of res_dtype (the same three)
+ *   seq_lens : NULL -> every sequence at seq_len; else [B] int32 on the
+ *              device (as kvdec_sparse_decode_kivi_varlen; seq_len ignored)
+ *   Other arguments and limits as kvdec_sparse_decode_kivi.  Both dtypes
+ *   KVDEC_F16 run exactly kvdec_sparse_decode_kivi / _varlen; any other
+ *   pair runs the generic kernel in fp32 arithmetic (one rounding of the
+ *   output to q_dtype).  No workspace.
+ */
+int kvdec_sparse_decode_kivi_typed(const void* q, const void* k_res, const void* v_res,
+                                   const void* const* kivi, void* o, int q_dtype, int res_dtype,
+                                   const int32_t* seq_lens, int64_t B, int32_t H, int32_t KVH,
+                                   int64_t seq_len, int32_t window, int32_t sink, int32_t residual,
+                                   int32_t group, int32_t bits, float sm_scale, void* stream);
+
+/*
  * Decode-time KIVI cache, the write side of the fused decode (no counterpart
  * in the reference, which builds the cache once per call:
  * quant_kernel.py:584-622).  State per (b, kv) head: the quantized sink

@@ -69,6 +69,9 @@ SIGNATURES = {
     "kvdec_sparse_decode_kivi_varlen": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _vp, _i64,
                                                        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                                        _vp]),
+    "kvdec_sparse_decode_kivi_typed": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, ctypes.c_int,
+                                                      ctypes.c_int, _vp, _i64, _i32, _i32, _i64, _i32, _i32,
+                                                      _i32, _i32, _i32, _f32, _vp]),
     "kvdec_kivi_stream_append": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.POINTER(_vp), _i64, _i32,
                                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "kvdec_kivi_stream_decode": (ctypes.c_int, [_vp, _vp, _vp, ctypes.POINTER(_vp), _vp, _i64, _i32,

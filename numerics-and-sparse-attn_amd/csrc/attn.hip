@@ -2367,14 +2367,20 @@ bool packed_group(int32_t H, int32_t KVH, int64_t window_old_groups) {
   return window_old_groups >= kPackMinGroups && KVH > 0 && H % KVH == 0 && H / KVH <= kPackGroup;
 }
 
-// Code widths and group sizes other than 2 / 32: the generic kernel, with
-// the reference's layout assumptions (whole bytes per group, channel groups
-// that divide the head dim).
+// The element types the attention entry points take (q, o and row caches).
+bool valid_attn_dtype(int dtype) { return dtype == KVDEC_F16 || dtype == KVDEC_F32 || dtype == KVDEC_BF16; }
+
+// Code widths and group sizes other than 2 / 32, and queries or residual
+// rows other than fp16: the generic kernel, with the reference's layout
+// assumptions (whole bytes per group, channel groups that divide the head
+// dim).
 int kivi_decode_generic(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
                         void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH,
                         int64_t seq_len, int32_t window, int32_t sink, int32_t residual, int32_t group,
-                        int32_t bits, float sm_scale, void* stream) {
+                        int32_t bits, float sm_scale, void* stream, int q_dtype = KVDEC_F16,
+                        int res_dtype = KVDEC_F16) {
   if (!q || !k_res || !v_res || !kivi || !o) return KVDEC_E_NULL;
+  if (!valid_attn_dtype(q_dtype) || !valid_attn_dtype(res_dtype)) return KVDEC_E_DTYPE;
   if (bits < 1 || bits > 8) return KVDEC_E_BITS;
   if (group < 1 || kHeadDim % group != 0 || group % (8 / bits) != 0) return KVDEC_E_GROUP;
   int rc = check_heads(B, H, KVH, kHeadDim);
@@ -2389,8 +2395,8 @@ int kivi_decode_generic(const void* q, const void* k_res, const void* v_res, con
   if (win_tok > 0)
     for (int i = 6; i < 12; ++i)
       if (!kivi[i]) return KVDEC_E_NULL;
-  return generic_kivi_decode(q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window, sink, res_rows,
-                             win_tok, group, bits, sm_scale, static_cast<hipStream_t>(stream));
+  return generic_kivi_decode(q, k_res, v_res, kivi, o, q_dtype, res_dtype, lens, B, H, KVH, seq_len, window,
+                             sink, res_rows, win_tok, group, bits, sm_scale, static_cast<hipStream_t>(stream));
 }
 
 int kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
@@ -2910,6 +2916,19 @@ int kvdec_sparse_decode_kivi_varlen(const void* q, const void* k_res, const void
   if (!seq_lens) return KVDEC_E_NULL;
   return kivi_decode(q, k_res, v_res, kivi, o, seq_lens, B, H, KVH, 1, window, sink, residual,
                      group, bits, sm_scale, stream);
+}
+
+int kvdec_sparse_decode_kivi_typed(const void* q, const void* k_res, const void* v_res,
+                                   const void* const* kivi, void* o, int q_dtype, int res_dtype,
+                                   const int32_t* seq_lens, int64_t B, int32_t H, int32_t KVH,
+                                   int64_t seq_len, int32_t window, int32_t sink, int32_t residual,
+                                   int32_t group, int32_t bits, float sm_scale, void* stream) {
+  const int64_t L = seq_lens ? 1 : seq_len;
+  if (q_dtype == KVDEC_F16 && res_dtype == KVDEC_F16)
+    return kivi_decode(q, k_res, v_res, kivi, o, seq_lens, B, H, KVH, L, window, sink, residual, group,
+                       bits, sm_scale, stream);
+  return kivi_decode_generic(q, k_res, v_res, kivi, o, seq_lens, B, H, KVH, L, window, sink, residual,
+                             group, bits, sm_scale, stream, q_dtype, res_dtype);
 }
 
 int kvdec_kivi_stream_decode(const void* q, const void* k_ring, const void* v_ring,

@@ -24,13 +24,14 @@ int generic_rows_decode(const void* q, const void* k, const void* v, void* o, in
                         void* ws, size_t ws_bytes, hipStream_t stream);
 
 // The fused KIVI decode for any code width (1..8 bits) and group size: q, o
-// fp16 [B, H, 128]; residual rows fp16 [B, KVH, res_rows, 128]; kivi[12] as
+// [B, H, 128] of q_dtype; residual rows [B, KVH, res_rows, 128] of
+// res_dtype (KVDEC_F16 / KVDEC_BF16 / KVDEC_F32 each); kivi[12] as
 // kvdec_sparse_decode_kivi (sink tensors of one padded group, window-old
 // tensors of win_tok tokens).  Slot validity: `lens` null -> the linear
 // sink + window rule at seq_len, else at lens[b] per sequence.
 int generic_kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
-                        void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH,
-                        int64_t seq_len, int32_t window, int32_t sink, int32_t res_rows,
+                        void* o, int q_dtype, int res_dtype, const int32_t* lens, int64_t B, int32_t H,
+                        int32_t KVH, int64_t seq_len, int32_t window, int32_t sink, int32_t res_rows,
                         int32_t win_tok, int32_t group, int32_t bits, float sm_scale,
                         hipStream_t stream);
 

@@ -108,11 +108,12 @@ struct GRowsSrc {
   }
 };
 
-// A KIVI cache of any width: residual fp16 rows and the quantized sink
-// (one group) and window-old (win_tok tokens) regions.
+// A KIVI cache of any width: residual rows of element type RT and the
+// quantized sink (one group) and window-old (win_tok tokens) regions.
+template <int RT>
 struct GKiviSrc {
-  const _Float16* kres;
-  const _Float16* vres;
+  const typename GElt<RT>::T* kres;
+  const typename GElt<RT>::T* vres;
   const uint8_t* kp[2];     // sink, window-old
   const _Float16* ks[2];
   const _Float16* kz[2];
@@ -127,8 +128,8 @@ struct GKiviSrc {
       const size_t base = ((size_t)pair * res_rows + (s - sink - win_tok)) * kHeadDim + c0;
 #pragma unroll
       for (int c = 0; c < 32; ++c) {
-        kk[c] = (float)kres[base + c];
-        vv[c] = (float)vres[base + c];
+        kk[c] = GElt<RT>::ld(kres, base + c);
+        vv[c] = GElt<RT>::ld(vres, base + c);
       }
       return;
     }
@@ -368,14 +369,14 @@ int generic_rows_decode(const void* q, const void* k, const void* v, void* o, in
   return KVDEC_E_DTYPE;
 }
 
-int generic_kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
-                        void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH,
-                        int64_t seq_len, int32_t window, int32_t sink, int32_t res_rows,
-                        int32_t win_tok, int32_t group, int32_t bits, float sm_scale,
-                        hipStream_t stream) {
-  GArgs<KVDEC_F16> A{};
-  A.q = static_cast<const _Float16*>(q);
-  A.o = static_cast<_Float16*>(o);
+template <int QT, int RT>
+int kivi_decode_t2(const void* q, const void* k_res, const void* v_res, const void* const* kivi, void* o,
+                   const int32_t* lens, int64_t B, int32_t H, int32_t KVH, int64_t seq_len, int32_t window,
+                   int32_t sink, int32_t res_rows, int32_t win_tok, int32_t group, int32_t bits,
+                   float sm_scale, hipStream_t stream) {
+  GArgs<QT> A{};
+  A.q = static_cast<const typename GElt<QT>::T*>(q);
+  A.o = static_cast<typename GElt<QT>::T*>(o);
   A.ws = nullptr;
   A.pairs = B * KVH;
   A.H = H;
@@ -387,9 +388,9 @@ int generic_kivi_decode(const void* q, const void* k_res, const void* v_res, con
                    KVDEC_LAYOUT_LINEAR, A.n_slots};
   A.n_splits = 1;
   A.per_split = ((A.n_slots + kGC - 1) / kGC) * kGC;
-  GKiviSrc S{};
-  S.kres = static_cast<const _Float16*>(k_res);
-  S.vres = static_cast<const _Float16*>(v_res);
+  GKiviSrc<RT> S{};
+  S.kres = static_cast<const typename GElt<RT>::T*>(k_res);
+  S.vres = static_cast<const typename GElt<RT>::T*>(v_res);
   for (int r = 0; r < 2; ++r) {
     const int base = 6 * r;
     S.kp[r] = static_cast<const uint8_t*>(kivi[base]);
@@ -407,6 +408,40 @@ int generic_kivi_decode(const void* q, const void* k_res, const void* v_res, con
   S.group = group;
   S.bits = bits;
   return launch_generic(A, S, stream);
+}
+
+template <int QT>
+int kivi_decode_q(int res_dtype, const void* q, const void* k_res, const void* v_res,
+                  const void* const* kivi, void* o, const int32_t* lens, int64_t B, int32_t H, int32_t KVH,
+                  int64_t seq_len, int32_t window, int32_t sink, int32_t res_rows, int32_t win_tok,
+                  int32_t group, int32_t bits, float sm_scale, hipStream_t stream) {
+  if (res_dtype == KVDEC_F16)
+    return kivi_decode_t2<QT, KVDEC_F16>(q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window, sink,
+                                         res_rows, win_tok, group, bits, sm_scale, stream);
+  if (res_dtype == KVDEC_BF16)
+    return kivi_decode_t2<QT, KVDEC_BF16>(q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window, sink,
+                                          res_rows, win_tok, group, bits, sm_scale, stream);
+  if (res_dtype == KVDEC_F32)
+    return kivi_decode_t2<QT, KVDEC_F32>(q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window, sink,
+                                         res_rows, win_tok, group, bits, sm_scale, stream);
+  return KVDEC_E_DTYPE;
+}
+
+int generic_kivi_decode(const void* q, const void* k_res, const void* v_res, const void* const* kivi,
+                        void* o, int q_dtype, int res_dtype, const int32_t* lens, int64_t B, int32_t H,
+                        int32_t KVH, int64_t seq_len, int32_t window, int32_t sink, int32_t res_rows,
+                        int32_t win_tok, int32_t group, int32_t bits, float sm_scale,
+                        hipStream_t stream) {
+  if (q_dtype == KVDEC_F16)
+    return kivi_decode_q<KVDEC_F16>(res_dtype, q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window,
+                                    sink, res_rows, win_tok, group, bits, sm_scale, stream);
+  if (q_dtype == KVDEC_BF16)
+    return kivi_decode_q<KVDEC_BF16>(res_dtype, q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window,
+                                     sink, res_rows, win_tok, group, bits, sm_scale, stream);
+  if (q_dtype == KVDEC_F32)
+    return kivi_decode_q<KVDEC_F32>(res_dtype, q, k_res, v_res, kivi, o, lens, B, H, KVH, seq_len, window,
+                                    sink, res_rows, win_tok, group, bits, sm_scale, stream);
+  return KVDEC_E_DTYPE;
 }
 
 }  // namespace kvdec

@@ -171,14 +171,17 @@ def sparse_decode_attention_quantized(
     quantize_k_cache / quantize_v_cache with the same arguments, the sink
     padded to one group) take the generic fp32 kernel: 1..8-bit codes,
     8 // bits per byte, groups that divide D_HEAD and hold whole bytes.
+    q and the residual may each be fp16, bf16 or fp32 (quant_kernel.py:
+    436-548 loads them in their own dtype); o has q's dtype.  Anything but
+    fp16 / fp16 takes the generic fp32 kernel.
     """
     tensors = dict(zip(_KIVI_ORDER, (k_sink_packed, k_sink_scale, k_sink_zero,
                                      v_sink_packed, v_sink_scale, v_sink_zero,
                                      k_win_packed, k_win_scale, k_win_zero,
                                      v_win_packed, v_win_scale, v_win_zero)))
-    _checks.require_gpu_tensor("q", q, ndim=3)
-    _checks.require_gpu_tensor("k_cache", k_cache, ndim=4)
-    _checks.require_gpu_tensor("v_cache", v_cache, ndim=4)
+    _checks.require_gpu_tensor("q", q, dtypes=tuple(_checks.ATTN_DTYPES), ndim=3)
+    _checks.require_gpu_tensor("k_cache", k_cache, dtypes=tuple(_checks.ATTN_DTYPES), ndim=4)
+    _checks.require_gpu_tensor("v_cache", v_cache, dtypes=(k_cache.dtype,), ndim=4)
     B, H, D = q.shape
     KVH = k_cache.shape[1]
     varlen = isinstance(seq_len, torch.Tensor)
@@ -218,6 +221,17 @@ def sparse_decode_attention_quantized(
     if sm_scale is None:
         sm_scale = D_HEAD**-0.5
     arr = (K._vp * 12)(*[K.ptr(tensors[n]) if tensors[n].numel() else None for n in _KIVI_ORDER])
+    if q.dtype != torch.float16 or k_cache.dtype != torch.float16:
+        # quant_kernel.py:436-548 loads q and the residual in their own dtype
+        # and stores o in q's: the generic kernel (fp32 arithmetic)
+        lens = K.ptr(seq_len) if varlen else None
+        rc = K.lib.kvdec_sparse_decode_kivi_typed(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), arr, K.ptr(o),
+                                                  _checks.ATTN_DTYPES[q.dtype],
+                                                  _checks.ATTN_DTYPES[k_cache.dtype], lens, B, H, KVH,
+                                                  1 if varlen else seq_len, window, sink, R, G, bits,
+                                                  float(sm_scale), K.stream_of(q))
+        K.check(rc, "sparse_decode_attention_quantized")
+        return o
     if varlen:
         rc = K.lib.kvdec_sparse_decode_kivi_varlen(K.ptr(q), K.ptr(k_cache), K.ptr(v_cache), arr, K.ptr(o),
                                                    K.ptr(seq_len), B, H, KVH, window, sink, R, G, bits,
@@ -244,7 +258,8 @@ def build_quantized_kv_cache(k_compacted, v_compacted, residual_size=RESIDUAL_SI
     -> fp32 is exact, so the codes equal the quantizers' on those copies).
     The residual keeps the input dtype, as in the reference, unless
     residual_dtype says otherwise (torch.float16 turns an fp32 or bf16 cache
-    into what the fused decode reads).  A window shorter than residual_size
+    into what the fp16 fused decode reads; a bf16 or fp32 residual takes the
+    generic fp32 kernel).  A window shorter than residual_size
     (undefined in the reference, whose slicing would then put sink slots into
     the residual) keeps the whole window as the residual and has no
     window-old part.

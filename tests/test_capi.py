@@ -35,7 +35,7 @@ def _header_codes():
 
 def test_header_and_binding_agree():
     funcs = _header_functions()
-    assert len(funcs) == 24
+    assert len(funcs) == 25
     assert funcs == sorted(K.SIGNATURES)
     assert _header_codes() == E
 
@@ -243,6 +243,33 @@ def test_kivi_varlen_validation():
     assert _kivi_varlen(W=0) == E["WINDOW"]
     assert _kivi_varlen(W=200) == E["GROUP"]
     assert _kivi_varlen(H=60) == E["SHAPE"]
+
+
+def _kivi_typed(**kw):
+    a = dict(q=FAKE, kr=FAKE, vr=FAKE, o=FAKE, qdt=K.BF16, rdt=K.F32, lens=None, B=32, H=64, KVH=8,
+             seq_len=163840, W=256, S=4, R=128, group=32, bits=2, scale=0.088, stream=None)
+    a.update(kw)
+    arr = (K._vp * 12)(*([0x1000] * 12))
+    return K.lib.kvdec_sparse_decode_kivi_typed(a["q"], a["kr"], a["vr"], arr, a["o"], a["qdt"], a["rdt"],
+                                                a["lens"], a["B"], a["H"], a["KVH"], a["seq_len"], a["W"],
+                                                a["S"], a["R"], a["group"], a["bits"], a["scale"],
+                                                a["stream"])
+
+
+def test_kivi_typed_validation():
+    assert _kivi_typed(q=None) == E["NULL"]
+    assert _kivi_typed(qdt=3) == E["DTYPE"]
+    assert _kivi_typed(rdt=-1) == E["DTYPE"]
+    assert _kivi_typed(qdt=K.F16, rdt=7) == E["DTYPE"]
+    assert _kivi_typed(bits=9) == E["BITS"]
+    assert _kivi_typed(group=48) == E["GROUP"]
+    assert _kivi_typed(W=200) == E["GROUP"]
+    assert _kivi_typed(seq_len=0) == E["SEQLEN"]
+    assert _kivi_typed(S=0) == E["WINDOW"]
+    assert _kivi_typed(KVH=3) == E["SHAPE"]
+    # fp16 / fp16 is the fused kernel's, with its checks
+    assert _kivi_typed(qdt=K.F16, rdt=K.F16, R=100) == E["WINDOW"]
+    assert _kivi_typed(qdt=K.F16, rdt=K.F16, q=None) == E["NULL"]
 
 
 def _quant(fn, **kw):

@@ -57,7 +57,7 @@ def _attend(q, c, L, W, S, R, group, bits):
         c["v_win_packed"], c["v_win_scale"], c["v_win_zero"],
         seq_len=L, window=W, sink=S, residual_size=R, group_size=group, bits=bits)
     torch.cuda.synchronize()
-    return host(o)
+    return host(o) if o.dtype == torch.float16 else _host_f32(o)
 
 
 @pytest.mark.parametrize("bits,group,W", [(4, 32, 256), (1, 16, 256), (8, 16, 512), (3, 64, 320),
@@ -165,6 +165,80 @@ def test_sparse_other_dtypes(dt, layout, device):
     torch.cuda.synchronize()
     ref = O.sparse_attention_varlen(qh, kh, vh, lens, W, S, SCALE, layout=lay)
     _check_dtype_output(_host_f32(o), ref, dt)
+
+
+def _check_typed_output(o, ref, dt):
+    if dt == "fp16":
+        assert_nearly_rounded(o, ref)
+    elif dt == "fp32":
+        # fp32 online softmax over logits up to ~10 in magnitude (the x10
+        # channel): a few fp32 ulps per logit, 1e-5 on outputs of order 1
+        assert max_abs(o, ref) < 1e-5
+    else:
+        _check_dtype_output(o, ref, dt)
+
+
+@pytest.mark.parametrize("q_dt,res_dt", [("bf16", "bf16"), ("fp32", "fp32"), ("fp16", "bf16"),
+                                         ("bf16", "fp16"), ("fp32", "fp16"), ("fp16", "fp32")])
+def test_quantized_attention_other_dtypes(q_dt, res_dt, device):
+    """q and the residual in bf16 / fp32 (quant_kernel.py:436-548 loads both
+    in their own dtype and stores o in q's): the cache built on the GPU from
+    a compacted cache of the residual's dtype equals the oracle's builder on
+    the same values, and the decode over it (steady state, ramp-up,
+    per-sequence lengths) is one rounding to q's dtype away from the oracle's
+    fp64 attention."""
+    from quant_kernel import build_quantized_kv_cache, sparse_decode_attention_quantized
+    B, H, KVH, D, S, R, W = 3, 64, 8, 128, 4, 128, 256
+    q = torch.from_numpy(randn((B, H, D), 120)).to(TORCH_DT[q_dt])
+    kc = torch.from_numpy(randn((B, KVH, S + W, D), 121))
+    kc[..., 3] *= 10
+    kc = kc.to(TORCH_DT[res_dt])
+    vc = torch.from_numpy(randn((B, KVH, S + W, D), 122)).to(TORCH_DT[res_dt])
+    qh = q.float().numpy()
+    hc = O.build_quantized_kv_cache(kc.float().numpy(), vc.float().numpy(), residual_size=R, sink=S)
+    say(f"kivi q={q_dt} residual={res_dt}")
+    c = build_quantized_kv_cache(kc.to(device), vc.to(device), residual_size=R, sink=S)
+    assert c["k_residual"].dtype == TORCH_DT[res_dt]
+    for key in O.CACHE_KEYS:
+        np.testing.assert_array_equal(_host_f32(c[key]), np.asarray(hc[key], dtype=np.float32), err_msg=key)
+    qd = q.to(device)
+
+    def attend(L):
+        o = sparse_decode_attention_quantized(
+            qd, c["k_residual"], c["v_residual"],
+            c["k_sink_packed"], c["k_sink_scale"], c["k_sink_zero"],
+            c["v_sink_packed"], c["v_sink_scale"], c["v_sink_zero"],
+            c["k_win_packed"], c["k_win_scale"], c["k_win_zero"],
+            c["v_win_packed"], c["v_win_scale"], c["v_win_zero"],
+            seq_len=L, window=W, sink=S, residual_size=R)
+        torch.cuda.synchronize()
+        assert o.dtype == TORCH_DT[q_dt]
+        return _host_f32(o)
+
+    for L in (163840, S + W - 37, 3):
+        ref = O.quantized_attention_masked(qh, hc, L, W, SCALE, sink=S, residual_size=R)
+        _check_typed_output(attend(L), ref, q_dt)
+    lens = np.array([163840, S + 40, 1], dtype=np.int32)
+    ref = O.quantized_attention_varlen(qh, hc, lens, W, SCALE, sink=S, residual_size=R)
+    _check_typed_output(attend(dev(lens, device)), ref, q_dt)
+
+
+@pytest.mark.parametrize("bits,group", [(4, 32), (3, 16)])
+def test_quantized_attention_other_dtypes_any_width(bits, group, device):
+    """bf16 q with an fp32 residual at code widths other than 2 bits."""
+    B, H, KVH, D, S, R, W = 2, 64, 8, 128, 4, 128, 320
+    kc = randn((B, KVH, S + W, D), 130 + bits).astype(np.float16)
+    vc = randn((B, KVH, S + W, D), 131 + bits).astype(np.float16)
+    q = torch.from_numpy(randn((B, H, D), 132 + bits)).to(torch.bfloat16)
+    say(f"kivi bf16 q, fp32 residual, bits={bits} group={group}")
+    hc, c = _quantized_cache(kc, vc, S, R, group, bits, device)
+    c["k_residual"], c["v_residual"] = c["k_residual"].float(), c["v_residual"].float()
+    qh = q.float().numpy()
+    for L in (163840, S + W - 37):
+        o = _attend(q.to(device), c, L, W, S, R, group, bits)
+        ref = O.quantized_attention_masked(qh, hc, L, W, SCALE, sink=S, residual_size=R, group_size=group,
+                                           bits=bits)
+        _check_dtype_output(o, ref, "bf16")
 
 
 def test_other_dtypes_rejected_where_fp16_only(device):
