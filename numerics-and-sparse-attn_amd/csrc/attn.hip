@@ -1584,8 +1584,10 @@ __device__ __forceinline__ void evict_group(const StepLeanArgs& A, uint32_t pair
 }
 __device__ __forceinline__ void evict_stage_k(const EvictK& kb, char* slot, int lane) {
 #pragma unroll
-  for (int p = 0; p < kTile / 4; ++p)
+  for (int p = 0; p < kTile / 4; ++p) {
     *reinterpret_cast<uint16_t*>(slot + kQsK + p * kQsKRow + 2 * lane) = (uint16_t)kb.rows[p];
+    *reinterpret_cast<uint16_t*>(slot + kQsK4 + p * kQsKRow + 2 * lane) = (uint16_t)(kb.rows[p] >> 4);
+  }
 }
 
 // f16_tile_step of a ring tile whose row rr (rr < 0: none) is replaced by

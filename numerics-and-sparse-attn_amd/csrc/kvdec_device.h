@@ -629,15 +629,20 @@ __device__ __forceinline__ void q_state_rescale(QState& qs, float alpha, int lan
 //                 transposed by ds_read_b64_tr_b8)
 //   [2816, 3072)  V scales transposed [4 groups][32 tokens],
 //   [3072, 3328)  negated V zeros transposed
+//   [3328, 4608)  the K code rows again, each 32-bit word shifted right by
+//                 4 bits (fields 2 and 3 of a byte at its bits 0..3)
 constexpr int kQsKRow = 160;
 constexpr int kQsK = 0, kQsKS = 1280, kQsKZ = 1536, kQsV = 1792, kQsVS = 2816, kQsVZ = 3072;
-constexpr int kQsBytes = 3328;
+constexpr int kQsK4 = 3328;
+constexpr int kQsBytes = 4608;
 static_assert(kQsBytes <= kSlotBytes, "a staged KIVI tile fits a wave slot");
 constexpr uint32_t kNegPk = 0x80008000u;   // sign bits of an fp16 pair
 constexpr uint32_t kOnePk = 0x3C003C00u;   // fp16 pair (1, 1)
 
 __device__ __forceinline__ void stage_q_raw(const QTileRaw& X, char* slot, int lane) {
   *reinterpret_cast<u32x4*>(slot + kQsK + kQsKRow * (lane >> 3) + 16 * (lane & 7)) = X.kc;
+  *reinterpret_cast<u32x4*>(slot + kQsK4 + kQsKRow * (lane >> 3) + 16 * (lane & 7)) =
+      u32x4{X.kc[0] >> 4, X.kc[1] >> 4, X.kc[2] >> 4, X.kc[3] >> 4};
   *reinterpret_cast<uint32_t*>(slot + kQsKS + 4 * lane) = X.ks;
   *reinterpret_cast<uint32_t*>(slot + kQsKZ + 4 * lane) = X.kz ^ kNegPk;
   *reinterpret_cast<u32x4*>(slot + kQsV + 16 * lane) = X.vc;
@@ -681,14 +686,11 @@ __device__ __forceinline__ u32x2 codes_f16(uint32_t c, float scale) {
                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c, scale, true))};
 }
 constexpr float kCodeScale = 512.0f;   // code * 2^-9 * 2^9 = code
-
-// The 2-bit fields at bit `sh` of every byte of the 8 bytes w, one per byte.
-// One 64-bit shift: bits that cross from w[1] into w[0] land above bit 1 of
-// byte 3 and are masked off.
-__device__ __forceinline__ u32x2 fields2(u32x2 w, uint32_t sh) {
-  const uint64_t x = ((uint64_t)w[1] << 32 | w[0]) >> sh;
-  return u32x2{(uint32_t)x & 0x03030303u, (uint32_t)(x >> 32) & 0x03030303u};
-}
+// A code at bits 2..3 of a byte whose other bits are zero reads, as an OCP
+// e4m3 byte, as code * 2^-7 (code 1 the subnormal 2^-7, codes 2 and 3 the
+// least normal binade's 2^-6 and 1.5 * 2^-6): such fields need no shift.
+constexpr float kCodeScale2 = 128.0f;
+constexpr uint32_t kField0 = 0x03030303u, kField1 = 0x0C0C0C0Cu;
 
 // |x| <= 2^(E - 15) (1 + m / 1024) for the fp16 bits x of exponent E and
 // mantissa m: the least el with |x| <= 2^el (for normal x).
@@ -812,7 +814,12 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
 
   // S[token][head] on MFMA: lane (t, g) feeds token 16 blk + t, channels
   // 32c + 8g .. +7 (code byte row (16 blk + t) / 4, bits 2 (t % 4)).
-  const uint32_t sh = 2u * (uint32_t)(t & 3);
+  // Fields 2 and 3 come from the rows shifted by 4 bits, so the lane's
+  // field sits at bits 0..1 (t even) or 2..3 (t odd) of each byte and is
+  // masked in place.
+  const uint32_t kmask = (t & 1) ? kField1 : kField0;
+  const float kcs = (t & 1) ? kCodeScale2 : kCodeScale;
+  const char* krow = slot + ((t & 2) ? kQsK4 : kQsK) + (t >> 2) * kQsKRow + 8 * g;
   float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
   float4v sz = {0.f, 0.f, 0.f, 0.f};   // the zero term of every token row
 #pragma unroll
@@ -826,10 +833,8 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
     if (!PACK) sz = mfma16x16x32(as_u4(nz[c]), ql, sz);
 #pragma unroll
     for (int blk = 0; blk < (HALF ? 1 : 2); ++blk) {
-      const u32x2 w =
-          *reinterpret_cast<const u32x2*>(slot + kQsK + (4 * blk + (t >> 2)) * kQsKRow + 32 * c + 8 * g);
-      const u32x2 f = fields2(w, sh);
-      const u32x2 d0 = codes_f16(f[0], kCodeScale), d1 = codes_f16(f[1], kCodeScale);
+      const u32x2 w = *reinterpret_cast<const u32x2*>(krow + 4 * blk * kQsKRow + 32 * c);
+      const u32x2 d0 = codes_f16(w[0] & kmask, kcs), d1 = codes_f16(w[1] & kmask, kcs);
       const u32x4 d = {d0[0], d0[1], d1[0], d1[1]};
       float4v& sb = blk == 0 ? s0 : s1;
       sb = mfma16x16x32(d, qx, sb);
@@ -915,12 +920,16 @@ __device__ __forceinline__ void q_tile_body(const char* slot, const half8 (&qB)[
                  fma_mix_pk_f16(pf[4], pf[5], vsc[2], pq[2]), fma_mix_pk_f16(pf[6], pf[7], vsc[3], pq[3])};
     }
     const half8 nzv = as_h8(u32x4{z_lo[0], z_lo[1], z_hi[0], z_hi[1]});
+    // fields vsh / 2 and vsh / 2 + 1 (m = 0, 1) from one shift, each masked
+    // in place (bits that cross words land above bit 3 of byte 3)
+    const uint64_t vx = ((uint64_t)vb[1] << 32 | vb[0]) >> vsh;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      const uint32_t s = vsh + 2u * (uint32_t)m;
-      const u32x2 c = HALF ? u32x2{(vb[0] >> s) & 0x03030303u, 0u} : fields2(vb, s);
-      const u32x2 b0 = codes_f16(c[0], kCodeScale);
-      const u32x2 b1 = HALF ? u32x2{0u, 0u} : codes_f16(c[1], kCodeScale);
+      const uint32_t msk = m ? kField1 : kField0;
+      const float csc = m ? kCodeScale2 : kCodeScale;
+      const u32x2 c = {(uint32_t)vx & msk, HALF ? 0u : (uint32_t)(vx >> 32) & msk};
+      const u32x2 b0 = codes_f16(c[0], csc);
+      const u32x2 b1 = HALF ? u32x2{0u, 0u} : codes_f16(c[1], csc);
       const half8 b = as_h8(u32x4{b0[0], b0[1], b1[0], b1[1]});
       float4v& acc = qs.O[2 * grp + m];
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(pq), b, acc, 0, 0, 0);
