@@ -165,7 +165,7 @@ def _capture(body, G):
     lib = CLOCK["lib"]
     log = None
     if lib is not None:
-        log = torch.zeros(CLOCK_LAUNCHES_PER_STEP * G * CLOCK_WGS * 2, dtype=torch.int64, device="cuda")
+        log = torch.zeros(CLOCK_LAUNCHES_PER_STEP * G * CLOCK_WGS * 4, dtype=torch.int64, device="cuda")
         if lib.kvdec_clock_arm(log.data_ptr(), CLOCK_LAUNCHES_PER_STEP * G) != 0:
             raise RuntimeError("kvdec_clock_arm failed")
     g = torch.cuda.CUDAGraph()
@@ -198,9 +198,10 @@ def _clock_stats(g, log):
     start and end.  Per launch: its own duration (last workgroup end - first
     workgroup start), the gap to the next launch (its first start - this
     launch's last end; negative = overlap), the dispatch ramp (last start -
-    first start) and the end spread (last end - first end), in us.  The
-    counter's rate is checked against HIP events around the same replay
-    (nominally 100 MHz)."""
+    first start) and the end spread (last end - first end), in us, and the
+    shader clock (MHz) of each workgroup: its core-clock ticks over its
+    realtime span.  The realtime counter's rate is checked against HIP
+    events around the same replay (nominally 100 MHz)."""
     log.zero_()
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
@@ -209,10 +210,11 @@ def _clock_stats(g, log):
     g.replay()
     e1.record()
     torch.cuda.synchronize()
-    a = log.cpu().numpy().view(np.uint64).reshape(-1, CLOCK_WGS, 2).astype(np.float64)
+    raw = log.cpu().numpy().view(np.uint64).reshape(-1, CLOCK_WGS, 4).astype(np.float64)
+    a, core = raw[:, :, :2], raw[:, :, 2:]
     live = a[:, :, 0] > 0                                # workgroups that ran
     keep = live.any(axis=1)
-    a, live = a[keep], live[keep]
+    a, core, live = a[keep], core[keep], live[keep]
     if len(a) < 2:
         return {"status": "no clocked launches recorded"}
     big = np.where(live, a[:, :, 0], np.inf)
@@ -228,6 +230,12 @@ def _clock_stats(g, log):
     gap = (first[1:] - last_end[:-1]) * tick_us
     ramp = (last_start - first) * tick_us
     tail = (last_end - first_end) * tick_us
+    # shader clock of each workgroup: core-clock ticks over its realtime span
+    # (spans of at least 1 us, where the 100 MHz counter's granularity is
+    # below 1%)
+    rt = (a[:, :, 1] - a[:, :, 0]) * tick_us
+    ok = live & (rt >= 1.0)
+    sclk = ((core[:, :, 1] - core[:, :, 0])[ok] / rt[ok]) if ok.any() else np.array([np.nan])
 
     def st(x):
         return {"mean": round(float(np.mean(x)), 3), "median": round(float(np.median(x)), 3),
@@ -235,7 +243,7 @@ def _clock_stats(g, log):
     return {"launches": int(len(a)), "workgroups_per_launch": int(live.sum(axis=1).max()),
             "counter_ticks_per_us_measured": round(rate, 2), "tick_us": tick_us,
             "kernel_us": st(span), "gap_us": st(gap), "overlapping_launches": int((gap < 0).sum()),
-            "dispatch_ramp_us": st(ramp), "end_spread_us": st(tail),
+            "dispatch_ramp_us": st(ramp), "end_spread_us": st(tail), "shader_clock_mhz": st(sclk),
             "first_start_to_last_end_us_per_launch": round(ticks * tick_us / len(a), 3)}
 
 

@@ -426,10 +426,11 @@ int kvdec_read_probe_sweep(const void* src, int64_t bytes, void* sink, int32_t b
  * Kernel clock, no counterpart in the reference.  In the timing build
  * (libkvdec_clock.so, the same sources compiled with -DKVDEC_CLOCK) every
  * attention-kernel launch after this call takes the next of `slots` slots
- * of `log` (cyclically): device memory of slots x 1024 x 2 uint64, zeroed
+ * of `log` (cyclically): device memory of slots x 1024 x 4 uint64, zeroed
  * by the caller.  Workgroup w < 1024 of the launch stores the GPU realtime
  * counter (100 MHz) at its start into [slot][w][0] and after its output
- * store into [slot][w][1].  log = NULL disarms.  The product library
+ * store into [slot][w][1], and the core-clock counter (s_memtime) at the
+ * same two points into [slot][w][2] and [slot][w][3].  log = NULL disarms.  The product library
  * returns KVDEC_E_UNSUPPORTED.
  */
 int kvdec_clock_arm(void* log, int32_t slots);

@@ -47,11 +47,12 @@ constexpr int kThreads = 64 * kWaves;
 // -DKVDEC_CLOCK; the product library has none of it).  Every launch of an
 // attention kernel gets slot `id` of a log armed by kvdec_clock_arm, with
 // one record per workgroup (the first kClockWgs): thread 0 stores the GPU's
-// constant-rate realtime counter when the workgroup starts and after its
-// output store, with plain vector stores (no atomics, no shared address).
-// The host reduces a slot to the launch's first start and last end, i.e.
-// its own duration with no profiler in the process, and the gap to the
-// next launch.
+// constant-rate realtime counter and its core-clock counter when the
+// workgroup starts and after its output store, with plain vector stores (no
+// atomics, no shared address).  The host reduces a slot to the launch's
+// first start and last end, i.e. its own duration with no profiler in the
+// process, and the gap to the next launch; the two counters' ratio is the
+// shader clock the launch ran at.
 #ifdef KVDEC_CLOCK
 constexpr int kClockWgs = 1024;
 struct ClockRef {
@@ -61,7 +62,10 @@ struct ClockRef {
 __device__ __forceinline__ void clock_stamp(const ClockRef& c, int end) {
   if (c.log != nullptr && threadIdx.x == 0 && blockIdx.x < (unsigned)kClockWgs) {
     const unsigned long long t = __builtin_amdgcn_s_memrealtime();
-    c.log[((size_t)c.id * kClockWgs + blockIdx.x) * 2 + end] = t;
+    const unsigned long long k = __builtin_amdgcn_s_memtime();
+    unsigned long long* rec = c.log + ((size_t)c.id * kClockWgs + blockIdx.x) * 4;
+    rec[end] = t;
+    rec[2 + end] = k;
   }
 }
 #define KVDEC_CLOCK_FIELD ClockRef clk;
